@@ -1,0 +1,101 @@
+"""Drop-in for ``gllm/model/layers/attention.py``: ``AttentionMetadata`` and
+``Attention`` with the hot path (RoPE, KV write, attention) on the HIP kernels.
+
+``Attention.forward`` keeps the reference's signature and semantics
+(``attention.py:122-182``): q/k/v projections, rotate-half RoPE, K/V written
+to the paged cache through ``query_slot_mapping``, attention of every real
+query row over its sequence's keys (mask ``p <= c_i + r``, the 0/-inf pattern
+of ``gllm/llm/llm.py:259-274``), then ``linear_o``.  The dense gather through
+``slot_mapping`` and the materialised ``bias`` are replaced by kernels that
+walk ``block_table``; q is rotated on load inside the attention kernel.
+Outputs of padded query rows (``r >= query_lens[i]``) are unspecified, as in
+the reference, where they attend to dummy slot 0.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from . import paged
+
+
+@dataclass
+class AttentionMetadata:
+    """Field-for-field ``attention.py:12-26`` plus the pool's ``block_size``
+    (the reference keeps it in ``GeneratorParams``; default 16)."""
+
+    query_lens: torch.Tensor            # [B] int32
+    seq_lens: torch.Tensor              # [B] int32
+    max_seq_len: int | torch.Tensor
+    block_table: torch.Tensor           # [B, max_num_blocks] int32
+    slot_mapping: torch.Tensor          # [B, T] int64 (unused by the kernels)
+    query_slot_mapping: torch.Tensor    # [B, T_q] int64
+    bias: torch.Tensor | None           # [B, T_q, T] (unused by the kernels)
+    block_size: int = 16
+
+
+def plan_for(meta: AttentionMetadata, *, num_q_heads: int, num_kv_heads: int, head_dim: int,
+             dtype: torch.dtype, device) -> paged.AttentionPlan:
+    """The batch plan, built once per metadata object (one engine step) and
+    reused by every layer.  Reads the lengths back once, like the reference's
+    own ``.tolist()`` / ``.item()`` calls in ``llm.py:166,176``."""
+    plan = getattr(meta, "_gllm_plan", None)
+    if plan is None:
+        ql = meta.query_lens.tolist()
+        sl = meta.seq_lens.tolist()
+        plan = paged.AttentionPlan(ql, sl, num_q_heads=num_q_heads, num_kv_heads=num_kv_heads,
+                                   head_dim=head_dim, block_size=meta.block_size, dtype=dtype,
+                                   device=device, q_seq_stride=meta.query_slot_mapping.shape[1])
+        object.__setattr__(meta, "_gllm_plan", plan)
+    return plan
+
+
+class Attention:
+    """``attention.py:30-182``.  ``weights`` maps the reference's safetensors
+    names (``model.layers.{i}.self_attn.{q,k,v,o}_proj.weight``) to tensors;
+    ``model_config`` needs ``dtype, hidden_size, head_dim, num_attn_heads,
+    num_kv_heads``."""
+
+    def __init__(self, layer_idx: int, model_config, safetensors):
+        self.layer_idx = layer_idx
+        self.num_q_heads = model_config.num_attn_heads
+        self.num_kv_heads = model_config.num_kv_heads
+        self.hidden_size = model_config.hidden_size
+        self.head_dim = model_config.head_dim
+        assert self.num_q_heads % self.num_kv_heads == 0
+        self.num_groups = self.num_q_heads // self.num_kv_heads
+        assert self.hidden_size == self.num_q_heads * self.head_dim
+        pre = f"model.layers.{layer_idx}.self_attn"
+        dt = model_config.dtype
+        self.W_q = safetensors[f"{pre}.q_proj.weight"].to(dtype=dt)
+        self.W_k = safetensors[f"{pre}.k_proj.weight"].to(dtype=dt)
+        self.W_v = safetensors[f"{pre}.v_proj.weight"].to(dtype=dt)
+        self.W_o = safetensors[f"{pre}.o_proj.weight"].to(dtype=dt)
+
+    def apply_rope(self, q: torch.Tensor, k: torch.Tensor, cos_pos: torch.Tensor, sin_pos: torch.Tensor):
+        """``attention.py:76-119`` (bit-identical rounding) on the HIP kernel."""
+        return paged.rope_rotate(q, cos_pos, sin_pos), paged.rope_rotate(k, cos_pos, sin_pos)
+
+    def forward(self, x: torch.Tensor, cos_pos: torch.Tensor, sin_pos: torch.Tensor,
+                kv_cache: torch.Tensor, attention_metadata: AttentionMetadata) -> torch.Tensor:
+        B, Tq, hidden = x.shape
+        assert hidden == self.hidden_size
+        Hq, Hkv, D = self.num_q_heads, self.num_kv_heads, self.head_dim
+        q = F.linear(x, self.W_q.to(x.device)).view(B, Tq, Hq, D)
+        k = F.linear(x, self.W_k.to(x.device)).view(B, Tq, Hkv, D)
+        v = F.linear(x, self.W_v.to(x.device)).view(B, Tq, Hkv, D)
+        attn = self.attention(q, k, v, cos_pos, sin_pos, kv_cache, attention_metadata)
+        return F.linear(attn.view(B, Tq, -1), self.W_o.to(x.device))
+
+    def attention(self, q, k, v, cos_pos, sin_pos, kv_cache, meta: AttentionMetadata) -> torch.Tensor:
+        """The hot path between the projections and ``linear_o``
+        (``attention.py:151-178``): returns ``[B, T_q, Hq, D]``."""
+        k_cache, v_cache = kv_cache[0], kv_cache[1]
+        paged.rope_kv_write(k, v, cos_pos, sin_pos, k_cache, v_cache, meta.query_slot_mapping,
+                            query_lens=meta.query_lens)
+        plan = plan_for(meta, num_q_heads=self.num_q_heads, num_kv_heads=self.num_kv_heads,
+                        head_dim=self.head_dim, dtype=q.dtype, device=q.device)
+        return paged.paged_attention(plan, q, k_cache, v_cache, meta.block_table,
+                                     rope=(cos_pos, sin_pos, "row"))

@@ -1,0 +1,385 @@
+// C ABI of libgllm_attn: argument validation, the host work planner and the
+// kernel launches.  Declarations and contracts: include/gllm_attn.h.
+#include <algorithm>
+#include <cstdarg>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/gllm_attn.h"
+#include "launch.h"
+
+using namespace gllm;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return GLLM_ATTN_OK;
+}
+
+int hip_check(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail(GLLM_ATTN_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+int log2i(int64_t x) {
+  int s = 0;
+  while ((int64_t(1) << s) < x) ++s;
+  return s;
+}
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+}  // namespace
+
+struct gllm_attn_plan {
+  int32_t num_seqs = 0, Hq = 0, Hkv = 0, D = 0, bs = 0, dtype = 0;
+  int32_t split_len = 0, max_q = 0;
+  int32_t n_decode_seqs = 0, n_prefill_seqs = 0;
+  int64_t total_rows = 0;
+  int64_t n_partials = 0;
+  std::vector<SeqInfo> seqs;
+  std::vector<WorkItem> items;
+  // staging copy of [items | seqs] in pinned host memory, device offsets
+  void* pinned = nullptr;
+  bool pinned_is_host_malloc = false;  // hipHostMalloc unavailable (no device): plain malloc
+  size_t off_items = 0, off_seqs = 0, off_ctr = 0, off_ml = 0, off_part = 0, ws_bytes = 0;
+  char* ws = nullptr;
+  hipEvent_t upload_done = nullptr;
+};
+
+extern "C" {
+
+const char* gllm_attn_last_error(void) { return g_last_error.c_str(); }
+int gllm_attn_version(void) { return 1; }
+
+int gllm_rope_kv_write(const void* q, void* q_out, const void* k, const void* v, void* k_cache,
+                       void* v_cache, const int64_t* slot_mapping, const int32_t* query_lens,
+                       int64_t tokens_per_seq, const void* cos, const void* sin,
+                       const int64_t* rope_rows, int64_t rope_row_stride, int64_t num_tokens,
+                       int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                       int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+                       int64_t q_out_row_stride, int64_t cache_slot_stride, int64_t num_slots,
+                       int32_t dtype, int32_t kv_dtype, void* stream) {
+  if (num_tokens < 0) return fail(GLLM_ATTN_EINVAL, "num_tokens < 0");
+  const bool kv = k || v;
+  if (!cos || !sin) return fail(GLLM_ATTN_EINVAL, "null cos/sin");
+  if (kv && (!k || !v || !k_cache || !v_cache || !slot_mapping))
+    return fail(GLLM_ATTN_EINVAL, "k, v, k_cache, v_cache and slot_mapping go together");
+  if (!kv && !q_out) return fail(GLLM_ATTN_EINVAL, "nothing to do: neither k/v nor q_out given");
+  if (q_out && !q) return fail(GLLM_ATTN_EINVAL, "q_out given without q");
+  if (num_kv_heads <= 0 || num_q_heads <= 0) return fail(GLLM_ATTN_EINVAL, "head counts must be > 0");
+  if (!((dtype == GLLM_DTYPE_BF16 && kv_dtype == GLLM_DTYPE_BF16) ||
+        (dtype == GLLM_DTYPE_F32 && (kv_dtype == GLLM_DTYPE_F32 || kv_dtype == GLLM_DTYPE_BF16))))
+    return fail(GLLM_ATTN_EUNSUPPORTED, "dtype/kv_dtype combination %d/%d not supported", dtype, kv_dtype);
+  const int vec = dtype == GLLM_DTYPE_F32 ? 4 : 8;
+  if (head_dim <= 0 || head_dim % (2 * vec) != 0)
+    return fail(GLLM_ATTN_EUNSUPPORTED, "head_dim %d must be a positive multiple of %d", head_dim, 2 * vec);
+  if (kv && (k_row_stride < (int64_t)num_kv_heads * head_dim || v_row_stride < (int64_t)num_kv_heads * head_dim))
+    return fail(GLLM_ATTN_EINVAL, "k/v row stride smaller than num_kv_heads * head_dim");
+  if (q_out && (q_row_stride < (int64_t)num_q_heads * head_dim || q_out_row_stride < (int64_t)num_q_heads * head_dim))
+    return fail(GLLM_ATTN_EINVAL, "q row stride smaller than num_q_heads * head_dim");
+  if (kv && cache_slot_stride < (int64_t)num_kv_heads * head_dim) return fail(GLLM_ATTN_EINVAL, "cache_slot_stride too small");
+  if (rope_row_stride < head_dim / 2) return fail(GLLM_ATTN_EINVAL, "rope_row_stride < head_dim / 2");
+  if (query_lens && tokens_per_seq <= 0) return fail(GLLM_ATTN_EINVAL, "tokens_per_seq must be > 0 with query_lens");
+  if (kv && num_slots <= 0) return fail(GLLM_ATTN_EINVAL, "num_slots must be > 0");
+  RopeKVWriteArgs a{};
+  a.q = q; a.q_out = q_out; a.k = k; a.v = v; a.k_cache = k_cache; a.v_cache = v_cache;
+  a.slot_mapping = slot_mapping; a.query_lens = query_lens; a.tokens_per_seq = tokens_per_seq;
+  a.cos = cos; a.sin = sin; a.rope_rows = rope_rows; a.rope_row_stride = rope_row_stride;
+  a.num_tokens = num_tokens; a.num_q_heads = num_q_heads; a.num_kv_heads = num_kv_heads; a.head_dim = head_dim;
+  a.q_row_stride = q_row_stride; a.k_row_stride = k_row_stride; a.v_row_stride = v_row_stride;
+  a.q_out_row_stride = q_out_row_stride; a.cache_slot_stride = cache_slot_stride; a.num_slots = num_slots;
+  a.dtype = dtype; a.kv_dtype = kv_dtype;
+  return hip_check(launch_rope_kv_write(a, (hipStream_t)stream), "rope_kv_write launch");
+}
+
+int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const int32_t* seq_lens,
+                          int32_t num_seqs, int64_t q_seq_stride, int32_t num_q_heads,
+                          int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t dtype,
+                          int32_t split_tokens) {
+  if (!out) return fail(GLLM_ATTN_EINVAL, "plan out-pointer is null");
+  *out = nullptr;
+  if (num_seqs < 0 || (num_seqs > 0 && (!query_lens || !seq_lens)))
+    return fail(GLLM_ATTN_EINVAL, "bad sequence arrays");
+  if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0)
+    return fail(GLLM_ATTN_EINVAL, "num_q_heads (%d) must be a positive multiple of num_kv_heads (%d)",
+                num_q_heads, num_kv_heads);
+  if (!is_pow2(block_size)) return fail(GLLM_ATTN_EUNSUPPORTED, "block_size %d is not a power of two", block_size);
+  if (dtype == GLLM_DTYPE_BF16) {
+    if (head_dim != 64 && head_dim != 128)
+      return fail(GLLM_ATTN_EUNSUPPORTED, "bf16 kernels support head_dim 64 and 128, not %d", head_dim);
+  } else if (dtype == GLLM_DTYPE_F32) {
+    if (head_dim <= 0 || head_dim > 256 || head_dim % 2) return fail(GLLM_ATTN_EUNSUPPORTED, "fp32 head_dim %d", head_dim);
+  } else {
+    return fail(GLLM_ATTN_EUNSUPPORTED, "dtype %d", dtype);
+  }
+  if (split_tokens < 0 || split_tokens % 32) return fail(GLLM_ATTN_EINVAL, "split_tokens must be a multiple of 32");
+  if (q_seq_stride < 0) return fail(GLLM_ATTN_EINVAL, "q_seq_stride < 0");
+  const int G = num_q_heads / num_kv_heads;
+
+  gllm_attn_plan* p = new (std::nothrow) gllm_attn_plan();
+  if (!p) return fail(GLLM_ATTN_EINVAL, "out of host memory");
+  p->num_seqs = num_seqs; p->Hq = num_q_heads; p->Hkv = num_kv_heads; p->D = head_dim;
+  p->bs = block_size; p->dtype = dtype;
+  p->seqs.resize(num_seqs);
+  int64_t row = 0, decode_tokens = 0;
+  for (int i = 0; i < num_seqs; ++i) {
+    const int32_t ql = query_lens[i], sl = seq_lens[i];
+    if (ql < 1 || sl < ql) {
+      delete p;
+      return fail(GLLM_ATTN_EINVAL, "sequence %d: query_len %d / seq_len %d invalid", i, ql, sl);
+    }
+    if (q_seq_stride > 0 && ql > q_seq_stride) {
+      delete p;
+      return fail(GLLM_ATTN_EINVAL, "sequence %d: query_len %d exceeds q_seq_stride %lld", i, ql, (long long)q_seq_stride);
+    }
+    SeqInfo& s = p->seqs[i];
+    s = SeqInfo{};
+    s.q_row_start = (int32_t)(q_seq_stride > 0 ? (int64_t)i * q_seq_stride : row);
+    s.ctx_len = sl - ql;
+    s.q_len = ql;
+    row += ql;
+    p->max_q = std::max(p->max_q, ql);
+    if (dtype == GLLM_DTYPE_BF16 && ql * G <= 16) decode_tokens += sl;
+  }
+  p->total_rows = q_seq_stride > 0 ? (int64_t)num_seqs * q_seq_stride : row;
+  if (p->total_rows > INT32_MAX) {
+    delete p;
+    return fail(GLLM_ATTN_EINVAL, "too many query rows");
+  }
+
+  if (dtype == GLLM_DTYPE_BF16) {
+    // Split length: aim for ~16 decode waves per CU, in multiples of 32 keys.
+    int cus = 256;
+    int dev = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0)
+      cus = prop.multiProcessorCount;
+    int64_t S = split_tokens;
+    if (S == 0) {
+      const int64_t target = (int64_t)cus * 16;
+      S = (decode_tokens * num_kv_heads + target - 1) / std::max<int64_t>(target, 1);
+      S = std::min<int64_t>(std::max<int64_t>((S + 31) / 32 * 32, 128), 8192);
+    }
+    p->split_len = (int32_t)S;
+    struct Keyed { int64_t work; WorkItem it; };
+    std::vector<Keyed> pf, dc;
+    const int kvg = (num_kv_heads + 3) / 4;
+    for (int i = 0; i < num_seqs; ++i) {
+      SeqInfo& s = p->seqs[i];
+      const int L = s.ctx_len + s.q_len;
+      if (s.q_len * G <= 16) {
+        ++p->n_decode_seqs;
+        s.nsplits = (int32_t)((L + S - 1) / S);
+        s.partial_base = (int32_t)p->n_partials;
+        if (s.nsplits > 1) p->n_partials += (int64_t)num_kv_heads * s.nsplits;
+        for (int sp = 0; sp < s.nsplits; ++sp)
+          for (int g4 = 0; g4 < kvg; ++g4) {
+            const int64_t keys = std::min<int64_t>(L, (int64_t)(sp + 1) * S) - (int64_t)sp * S;
+            dc.push_back({keys, WorkItem{kItemDecode, i, sp, g4}});
+          }
+      } else {
+        ++p->n_prefill_seqs;
+        const int nrb = (s.q_len + 31) / 32;
+        const int nwg = (G * nrb + 3) / 4;
+        for (int h = 0; h < num_kv_heads; ++h)
+          for (int w = 0; w < nwg; ++w) {
+            const int last_combo = std::min(w * 4 + 3, G * nrb - 1);
+            const int64_t kend = s.ctx_len + std::min(s.q_len - 1, (last_combo / G) * 32 + 31) + 1;
+            pf.push_back({kend, WorkItem{kItemPrefill, i, h, w}});
+          }
+      }
+    }
+    // Longest work first so the tail is made of short items.
+    std::stable_sort(pf.begin(), pf.end(), [](const Keyed& x, const Keyed& y) { return x.work > y.work; });
+    std::stable_sort(dc.begin(), dc.end(), [](const Keyed& x, const Keyed& y) { return x.work > y.work; });
+    p->items.reserve(pf.size() + dc.size());
+    for (auto& k : pf) p->items.push_back(k.it);
+    for (auto& k : dc) p->items.push_back(k.it);
+    if (p->items.size() > (size_t)INT32_MAX) {
+      delete p;
+      return fail(GLLM_ATTN_EINVAL, "too many work items");
+    }
+  }
+
+  // Workspace layout: items | seqs | tickets | partial (m, l) | partial acc.
+  size_t o = 0;
+  p->off_items = o; o = align256(o + p->items.size() * sizeof(WorkItem));
+  p->off_seqs = o; o = align256(o + p->seqs.size() * sizeof(SeqInfo));
+  p->off_ctr = o; o = align256(o + (size_t)num_seqs * num_kv_heads * sizeof(int32_t));
+  p->off_ml = o; o = align256(o + (size_t)p->n_partials * 16 * 2 * sizeof(float));
+  p->off_part = o; o = align256(o + (size_t)p->n_partials * 16 * head_dim * sizeof(float));
+  p->ws_bytes = std::max<size_t>(o, 256);
+  const size_t stage = p->off_ctr;
+  if (stage > 0) {
+    if (hipHostMalloc(&p->pinned, stage, hipHostMallocDefault) != hipSuccess) {
+      (void)hipGetLastError();
+      p->pinned = std::malloc(stage);
+      p->pinned_is_host_malloc = true;
+      if (!p->pinned) {
+        delete p;
+        return fail(GLLM_ATTN_EINVAL, "out of host memory for %zu staging bytes", stage);
+      }
+    }
+    std::memset(p->pinned, 0, stage);
+    if (!p->items.empty()) std::memcpy((char*)p->pinned + p->off_items, p->items.data(), p->items.size() * sizeof(WorkItem));
+    if (!p->seqs.empty()) std::memcpy((char*)p->pinned + p->off_seqs, p->seqs.data(), p->seqs.size() * sizeof(SeqInfo));
+  }
+  *out = p;
+  return ok();
+}
+
+size_t gllm_attn_plan_workspace_bytes(const gllm_attn_plan* p) { return p ? p->ws_bytes : 0; }
+
+int gllm_attn_plan_info(const gllm_attn_plan* p, int64_t* info, int32_t n) {
+  if (!p || !info) return fail(GLLM_ATTN_EINVAL, "null plan or info");
+  const int64_t v[6] = {(int64_t)p->items.size(), p->split_len, p->n_decode_seqs, p->n_prefill_seqs,
+                        p->n_partials, p->total_rows};
+  for (int i = 0; i < n && i < 6; ++i) info[i] = v[i];
+  return ok();
+}
+
+int gllm_attn_plan_upload(gllm_attn_plan* p, void* workspace, size_t bytes, void* stream) {
+  if (!p) return fail(GLLM_ATTN_EINVAL, "null plan");
+  if (!workspace || bytes < p->ws_bytes)
+    return fail(GLLM_ATTN_EINVAL, "workspace of %zu bytes is smaller than the %zu the plan needs", bytes, p->ws_bytes);
+  if (((uintptr_t)workspace & 255) != 0) return fail(GLLM_ATTN_EINVAL, "workspace must be 256-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  p->ws = (char*)workspace;
+  if (p->off_ctr > 0) {
+    hipError_t e = hipMemcpyAsync(p->ws, p->pinned, p->off_ctr, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return hip_check(e, "plan upload copy");
+  }
+  hipError_t e = launch_fill_zero_i32((int32_t*)(p->ws + p->off_ctr), (int64_t)p->num_seqs * p->Hkv, st);
+  if (e != hipSuccess) return hip_check(e, "ticket clear");
+  if (!p->upload_done) {
+    e = hipEventCreateWithFlags(&p->upload_done, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_check(e, "hipEventCreate");
+  }
+  return hip_check(hipEventRecord(p->upload_done, st), "hipEventRecord");
+}
+
+int gllm_attn_plan_destroy(gllm_attn_plan* p) {
+  if (!p) return ok();
+  if (p->upload_done) {
+    hipEventSynchronize(p->upload_done);  // the staging copy must finish before the free
+    hipEventDestroy(p->upload_done);
+  }
+  if (p->pinned) {
+    if (p->pinned_is_host_malloc)
+      std::free(p->pinned);
+    else
+      hipHostFree(p->pinned);
+  }
+  delete p;
+  return ok();
+}
+
+static int fill_common(AttnArgs& a, int32_t Hq, int32_t Hkv, int32_t D, float scale, int32_t dtype, int32_t kv_dtype) {
+  a.num_q_heads = Hq; a.num_kv_heads = Hkv; a.head_dim = D;
+  a.scale = scale; a.dtype = dtype; a.kv_dtype = kv_dtype;
+  if (!(scale > 0.f) || !std::isfinite(scale)) return fail(GLLM_ATTN_EINVAL, "scale must be finite and > 0");
+  return ok();
+}
+
+int gllm_paged_attention(const gllm_attn_plan* p, const void* q, int64_t q_row_stride, void* out,
+                         int64_t out_row_stride, const void* k_cache, const void* v_cache,
+                         int64_t cache_slot_stride, int64_t num_blocks, const int32_t* block_table,
+                         int64_t block_table_stride, const void* rope_cos, const void* rope_sin,
+                         int64_t rope_row_stride, int32_t rope_mode, float scale, int32_t dtype,
+                         int32_t kv_dtype, void* stream) {
+  if (!p) return fail(GLLM_ATTN_EINVAL, "null plan");
+  if (!p->ws) return fail(GLLM_ATTN_EINVAL, "plan was not uploaded (gllm_attn_plan_upload)");
+  if (dtype != p->dtype) return fail(GLLM_ATTN_EINVAL, "dtype %d differs from the plan's %d", dtype, p->dtype);
+  if (!q || !out || !k_cache || !v_cache || !block_table) return fail(GLLM_ATTN_EINVAL, "null pointer argument");
+  const int64_t hd = (int64_t)p->Hq * p->D;
+  if (q_row_stride < hd || out_row_stride < hd) return fail(GLLM_ATTN_EINVAL, "q/out row stride < num_q_heads * head_dim");
+  if (cache_slot_stride < (int64_t)p->Hkv * p->D) return fail(GLLM_ATTN_EINVAL, "cache_slot_stride too small");
+  if (num_blocks <= 0) return fail(GLLM_ATTN_EINVAL, "num_blocks must be > 0");
+  if (block_table_stride <= 0) return fail(GLLM_ATTN_EINVAL, "block_table_stride must be > 0");
+  if (rope_mode != GLLM_ROPE_NONE && rope_mode != GLLM_ROPE_BY_POSITION && rope_mode != GLLM_ROPE_BY_ROW)
+    return fail(GLLM_ATTN_EINVAL, "rope_mode %d", rope_mode);
+  if (rope_mode != GLLM_ROPE_NONE && (!rope_cos || !rope_sin || rope_row_stride < p->D / 2))
+    return fail(GLLM_ATTN_EINVAL, "rope tables missing or row stride < head_dim / 2");
+  if (dtype == GLLM_DTYPE_BF16 && kv_dtype != GLLM_DTYPE_BF16)
+    return fail(GLLM_ATTN_EUNSUPPORTED, "bf16 model dtype needs a bf16 KV cache");
+  if (dtype == GLLM_DTYPE_F32 && kv_dtype != GLLM_DTYPE_F32 && kv_dtype != GLLM_DTYPE_BF16)
+    return fail(GLLM_ATTN_EUNSUPPORTED, "kv_dtype %d", kv_dtype);
+  AttnArgs a{};
+  if (int rc = fill_common(a, p->Hq, p->Hkv, p->D, scale, dtype, kv_dtype)) return rc;
+  a.q = q; a.q_row_stride = q_row_stride; a.out = out; a.out_row_stride = out_row_stride;
+  a.k_cache = k_cache; a.v_cache = v_cache; a.cache_slot_stride = cache_slot_stride; a.num_blocks = num_blocks;
+  a.block_table = block_table; a.block_table_stride = block_table_stride;
+  a.block_size = p->bs; a.block_shift = log2i(p->bs);
+  a.rope_cos = rope_cos; a.rope_sin = rope_sin; a.rope_row_stride = rope_row_stride; a.rope_mode = rope_mode;
+  a.seqs = (const SeqInfo*)(p->ws + p->off_seqs);
+  a.items = (const WorkItem*)(p->ws + p->off_items);
+  a.n_items = (int32_t)p->items.size();
+  a.num_seqs = p->num_seqs;
+  a.counters = (int32_t*)(p->ws + p->off_ctr);
+  a.partial_ml = (float*)(p->ws + p->off_ml);
+  a.partials = (float*)(p->ws + p->off_part);
+  a.split_len = p->split_len;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == GLLM_DTYPE_BF16)
+    return hip_check(launch_paged_attention_bf16(a, p->n_prefill_seqs > 0, p->n_decode_seqs > 0, st),
+                     "paged attention launch");
+  return hip_check(launch_attention_f32(a, false, p->num_seqs, p->max_q, st), "fp32 attention launch");
+}
+
+int gllm_attention_dense(const void* q, int64_t q_row_stride, const void* k, int64_t k_batch_stride,
+                         int64_t k_row_stride, const void* v, int64_t v_batch_stride, int64_t v_row_stride,
+                         const void* bias, int64_t bias_batch_stride, int64_t bias_row_stride, void* out,
+                         int64_t out_row_stride, int32_t batch, int32_t q_len, int32_t kv_len,
+                         int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
+                         int32_t dtype, void* stream) {
+  if (!q || !k || !v || !bias || !out) return fail(GLLM_ATTN_EINVAL, "null pointer argument");
+  if (batch < 0 || q_len < 0 || kv_len < 0) return fail(GLLM_ATTN_EINVAL, "negative size");
+  if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads)
+    return fail(GLLM_ATTN_EINVAL, "num_q_heads (%d) must be a positive multiple of num_kv_heads (%d)", num_q_heads, num_kv_heads);
+  const int64_t hd = (int64_t)num_q_heads * head_dim;
+  if (q_row_stride < hd || out_row_stride < hd) return fail(GLLM_ATTN_EINVAL, "q/out row stride too small");
+  if (k_row_stride < (int64_t)num_kv_heads * head_dim || v_row_stride < (int64_t)num_kv_heads * head_dim)
+    return fail(GLLM_ATTN_EINVAL, "k/v row stride too small");
+  if (bias_row_stride < kv_len) return fail(GLLM_ATTN_EINVAL, "bias row stride < kv_len");
+  if (dtype == GLLM_DTYPE_BF16) {
+    if (head_dim != 64 && head_dim != 128)
+      return fail(GLLM_ATTN_EUNSUPPORTED, "bf16 kernels support head_dim 64 and 128, not %d", head_dim);
+  } else if (dtype == GLLM_DTYPE_F32) {
+    if (head_dim <= 0 || head_dim > 256) return fail(GLLM_ATTN_EUNSUPPORTED, "fp32 head_dim %d", head_dim);
+  } else {
+    return fail(GLLM_ATTN_EUNSUPPORTED, "dtype %d", dtype);
+  }
+  if (kv_len == 0 && batch * q_len > 0) return fail(GLLM_ATTN_EINVAL, "kv_len == 0 (softmax over no keys)");
+  AttnArgs a{};
+  if (int rc = fill_common(a, num_q_heads, num_kv_heads, head_dim, scale, dtype, dtype)) return rc;
+  a.q = q; a.q_row_stride = q_row_stride; a.out = out; a.out_row_stride = out_row_stride;
+  a.k = k; a.v = v; a.k_batch_stride = k_batch_stride; a.k_row_stride = k_row_stride;
+  a.v_batch_stride = v_batch_stride; a.v_row_stride = v_row_stride;
+  a.bias = bias; a.bias_batch_stride = bias_batch_stride; a.bias_row_stride = bias_row_stride;
+  a.dense_T = kv_len; a.dense_Tq = q_len;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == GLLM_DTYPE_BF16) return hip_check(launch_dense_attention_bf16(a, batch, q_len, st), "dense attention launch");
+  return hip_check(launch_attention_f32(a, true, batch, q_len, st), "fp32 dense attention launch");
+}
+
+}  // extern "C"

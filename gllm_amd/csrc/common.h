@@ -1,0 +1,125 @@
+// Shared device helpers for the gfx950 (CDNA4) attention kernels.
+//
+// Lane layouts below were checked on an MI355X with an in-bounds probe:
+//   v_mfma_f32_16x16x32_bf16: A[m=l%16][k=8*(l/16)+i], B[k=8*(l/16)+i][n=l%16],
+//                             C[m=4*(l/16)+j][n=l%16]            (i<8, j<4)
+//   v_mfma_f32_32x32x16_bf16: A[m=l%32][k=8*(l/32)+i], B[k=8*(l/32)+i][n=l%32],
+//                             C[m=8*(j/4)+4*(l/32)+j%4][n=l%32]  (i<8, j<16)
+//   ds_read_b64_tr_b16 (per 16-lane group, lane s supplies 4 x 16-bit D[s][0..3]):
+//                             lane i receives D[4*j + i/4][i%4], j = 0..3
+//   permlane16_swap(x, x) / permlane32_swap(x, x): max(r0, r1) is the max of x
+//                             over lanes {l, l^16} / {l, l^32}.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gllm {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) short i16x4;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// ---------------------------------------------------------------- bf16 bits
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 bits (quiet NaN kept NaN), the rounding
+// torch applies when it stores a bf16 result.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+// 8 fp32 -> one MFMA operand of 8 bf16.
+__device__ __forceinline__ bf16x8 to_bf16x8(const float* v) {
+  u32x4 w;
+  w[0] = pack_bf16x2(v[0], v[1]);
+  w[1] = pack_bf16x2(v[2], v[3]);
+  w[2] = pack_bf16x2(v[4], v[5]);
+  w[3] = pack_bf16x2(v[6], v[7]);
+  return __builtin_bit_cast(bf16x8, w);
+}
+
+__device__ __forceinline__ void unpack_bf16x8(const u32x4 w, float* v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(w[i] << 16);
+    v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+// ---------------------------------------------------------------- memory
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
+
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// Transposed LDS read: see the layout note at the top of this file.
+__device__ __forceinline__ u32x2 lds_read_tr16(const void* lds_addr) {
+  i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)const_cast<void*>(lds_addr));
+  return __builtin_bit_cast(u32x2, r);
+}
+
+// ---------------------------------------------------------------- MFMA
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------- cross-lane
+__device__ __forceinline__ float max_xor16(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Sequence / work descriptors shared by host planner and kernels.
+struct SeqInfo {
+  int32_t q_row_start;   // first query row of the sequence in q / out
+  int32_t ctx_len;       // c_i = seq_len - query_len
+  int32_t q_len;         // q_i
+  int32_t nsplits;       // decode-path splits (0 for prefill-path sequences)
+  int32_t partial_base;  // first partial index of (seq, kv head 0, split 0)
+  int32_t pad0, pad1, pad2;
+};
+
+enum : int32_t { kItemPrefill = 0, kItemDecode = 1 };
+
+struct WorkItem {
+  int32_t kind;   // kItemPrefill / kItemDecode
+  int32_t seq;
+  int32_t a;      // prefill: kv head;       decode: split index
+  int32_t b;      // prefill: wave-group id; decode: kv-head group (4 heads)
+};
+
+}  // namespace gllm

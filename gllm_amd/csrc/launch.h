@@ -1,0 +1,83 @@
+// Host-visible argument blocks and launchers shared by the C ABI and kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.h"
+
+namespace gllm {
+
+enum : int32_t { kF32 = 0, kBF16 = 1 };
+
+struct RopeKVWriteArgs {
+  const void* q;            // [N, q_row_stride] model dtype, heads at h*D
+  void* q_out;              // nullable: rotated q (same layout, q_out_row_stride)
+  const void* k;            // [N, k_row_stride]
+  const void* v;            // [N, v_row_stride]
+  void* k_cache;            // [num_slots, cache_slot_stride] kv dtype
+  void* v_cache;
+  const int64_t* slot_mapping;   // [N]
+  const int32_t* query_lens;     // nullable: skip row r >= query_lens[tok / tokens_per_seq]
+  int64_t tokens_per_seq;
+  const void* cos;               // [rows, rope_row_stride] model dtype
+  const void* sin;
+  const int64_t* rope_rows;      // nullable: cos/sin row per token (else the token index)
+  int64_t rope_row_stride;
+  int64_t num_tokens;
+  int32_t num_q_heads, num_kv_heads, head_dim;
+  int64_t q_row_stride, k_row_stride, v_row_stride, q_out_row_stride;
+  int64_t cache_slot_stride, num_slots;
+  int32_t dtype, kv_dtype;
+};
+
+enum : int32_t { kRopeNone = 0, kRopeByPosition = 1, kRopeByRow = 2 };
+
+// Paged attention (decode / prefill / mixed) and the dense-bias op share it.
+struct AttnArgs {
+  const void* q;             // query rows, heads at h*D within a row
+  int64_t q_row_stride;      // elements between consecutive query rows
+  void* out;
+  int64_t out_row_stride;
+  // paged source
+  const void* k_cache;
+  const void* v_cache;
+  int64_t cache_slot_stride;  // elements between slots (Hkv * D)
+  int64_t num_blocks;
+  const int32_t* block_table;
+  int64_t block_table_stride;
+  int32_t block_size;
+  int32_t block_shift;        // log2(block_size) (block_size is a power of two)
+  // dense source (reference_attention contract); q/out rows are b * q_seq_stride + r
+  const void* k;
+  const void* v;
+  int64_t k_batch_stride, k_row_stride, v_batch_stride, v_row_stride;
+  const void* bias;           // [B, T_q, T] model dtype
+  int64_t bias_batch_stride, bias_row_stride;
+  int32_t dense_T;            // keys per batch entry
+  int32_t dense_Tq;           // query rows per batch entry (q/out row = b * dense_Tq + r)
+  // rope applied to q on load
+  const void* rope_cos;
+  const void* rope_sin;
+  int64_t rope_row_stride;
+  int32_t rope_mode;
+  // work description
+  const SeqInfo* seqs;
+  const WorkItem* items;
+  int32_t n_items;
+  int32_t num_seqs;
+  float* partials;            // [n_partials][16][D] fp32
+  float* partial_ml;          // [n_partials][16][2] fp32 (running max in log2 units, sum)
+  int32_t* counters;          // [num_seqs * Hkv] split tickets, zero between launches
+  int32_t split_len;
+  int32_t num_q_heads, num_kv_heads, head_dim;
+  float scale;
+  int32_t dtype, kv_dtype;
+};
+
+hipError_t launch_rope_kv_write(const RopeKVWriteArgs& a, hipStream_t stream);
+hipError_t launch_paged_attention_bf16(const AttnArgs& a, bool has_prefill, bool has_decode, hipStream_t stream);
+hipError_t launch_dense_attention_bf16(const AttnArgs& a, int B, int Tq, hipStream_t stream);
+hipError_t launch_attention_f32(const AttnArgs& a, bool dense, int B, int max_q, hipStream_t stream);
+hipError_t launch_fill_zero_i32(int32_t* p, int64_t n, hipStream_t stream);
+
+}  // namespace gllm

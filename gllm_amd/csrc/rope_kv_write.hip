@@ -1,0 +1,146 @@
+// Fused rotate-half RoPE + paged KV-cache write.
+//
+// Replaces gllm/model/layers/attention.py:151-161 (apply_rope on k, the
+// index_put_ of k/v through query_slot_mapping) and, optionally, the q half
+// of apply_rope (attention.py:76-119).  Every arithmetic step is rounded to
+// the model dtype in the same order as the reference's torch ops, so the
+// written K rows are bit-identical to the reference's (no FMA contraction:
+// this unit is compiled with -ffp-contract=off and uses explicit rounding).
+#include "common.h"
+#include "launch.h"
+
+namespace gllm {
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static constexpr int kVec = 4;  // elements per 16-byte vector
+  __device__ static void load(const void* p, float* v) {
+    u32x4 w = ld16(p);
+    for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(w[i]);
+  }
+  __device__ static float mul(float a, float b) { return __fmul_rn(a, b); }
+  __device__ static float add(float a, float b) { return __fadd_rn(a, b); }
+  __device__ static float sub(float a, float b) { return __fsub_rn(a, b); }
+};
+template <> struct Elem<__bf16> {
+  static constexpr int kVec = 8;
+  __device__ static void load(const void* p, float* v) { unpack_bf16x8(ld16(p), v); }
+  // bf16 x bf16 is exact in fp32; the store rounds once (RNE), like torch.
+  __device__ static float mul(float a, float b) { return round_bf16(__fmul_rn(a, b)); }
+  __device__ static float add(float a, float b) { return round_bf16(__fadd_rn(a, b)); }
+  __device__ static float sub(float a, float b) { return round_bf16(__fsub_rn(a, b)); }
+};
+
+// Store `n` values (already representable in T when T is the model dtype)
+// as element type S at p.
+template <typename S> __device__ void store_vals(void* p, const float* v, int n);
+template <> __device__ void store_vals<float>(void* p, const float* v, int n) {
+  float* o = reinterpret_cast<float*>(p);
+  if (n == 4) {
+    u32x4 w;
+    for (int i = 0; i < 4; ++i) w[i] = __float_as_uint(v[i]);
+    st16(o, w);
+  } else {
+    for (int i = 0; i < n; ++i) o[i] = v[i];
+  }
+}
+template <> __device__ void store_vals<__bf16>(void* p, const float* v, int n) {
+  if (n == 8) {
+    u32x4 w;
+    for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+    st16(p, w);
+  } else {  // n == 4
+    u32x2 w;
+    for (int i = 0; i < 2; ++i) w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+    st8(p, w);
+  }
+}
+
+template <typename T, typename KV>
+__global__ void __launch_bounds__(256) rope_kv_write_kernel(RopeKVWriteArgs a) {
+  constexpr int V = Elem<T>::kVec;
+  const int D = a.head_dim, half = D / 2;
+  const int pv = half / V;          // vectors per half head
+  const int dv = D / V;             // vectors per head
+  const int k_items = a.k ? a.num_kv_heads * pv : 0;
+  const int v_items = a.k ? a.num_kv_heads * dv : 0;
+  const int q_items = a.q_out ? a.num_q_heads * pv : 0;
+  const int per_tok = k_items + v_items + q_items;
+  const int64_t total = a.num_tokens * (int64_t)per_tok;
+  for (int64_t it = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; it < total;
+       it += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t tok = it / per_tok;
+    int u = (int)(it - tok * per_tok);
+    int64_t slot = -1;
+    bool write_kv = u < k_items + v_items;
+    if (write_kv) {
+      if (a.query_lens) {
+        int64_t b = tok / a.tokens_per_seq, r = tok - b * a.tokens_per_seq;
+        if (r >= a.query_lens[b]) continue;            // padded row: nothing to write
+      }
+      slot = a.slot_mapping[tok];
+      if (slot < 0 || slot >= a.num_slots) continue;   // never write out of the pool
+    }
+    const int64_t crow = a.rope_rows ? a.rope_rows[tok] : tok;
+    const char* cosp = reinterpret_cast<const char*>(a.cos) + crow * a.rope_row_stride * sizeof(T);
+    const char* sinp = reinterpret_cast<const char*>(a.sin) + crow * a.rope_row_stride * sizeof(T);
+    if (u < k_items || u >= k_items + v_items) {
+      // rotate one vector of pairs (x[j], x[j + D/2]) of K or Q
+      bool is_q = u >= k_items + v_items;
+      int uu = is_q ? u - k_items - v_items : u;
+      int h = uu / pv, j0 = (uu - h * pv) * V;
+      const char* src = reinterpret_cast<const char*>(is_q ? a.q : a.k) +
+                        (tok * (is_q ? a.q_row_stride : a.k_row_stride) + (int64_t)h * D) * sizeof(T);
+      float x1[V], x2[V], c[V], s[V], lo[V], hi[V];
+      Elem<T>::load(src + j0 * sizeof(T), x1);
+      Elem<T>::load(src + (j0 + half) * sizeof(T), x2);
+      Elem<T>::load(cosp + j0 * sizeof(T), c);
+      Elem<T>::load(sinp + j0 * sizeof(T), s);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        // attention.py:105-118: [x1*c - x2*s, x1*s + x2*c], each op in T
+        lo[i] = Elem<T>::sub(Elem<T>::mul(x1[i], c[i]), Elem<T>::mul(x2[i], s[i]));
+        hi[i] = Elem<T>::add(Elem<T>::mul(x1[i], s[i]), Elem<T>::mul(x2[i], c[i]));
+      }
+      if (is_q) {
+        char* dst = reinterpret_cast<char*>(a.q_out) + (tok * a.q_out_row_stride + (int64_t)h * D) * sizeof(T);
+        store_vals<T>(dst + j0 * sizeof(T), lo, V);
+        store_vals<T>(dst + (j0 + half) * sizeof(T), hi, V);
+      } else {
+        char* dst = reinterpret_cast<char*>(a.k_cache) + (slot * a.cache_slot_stride + (int64_t)h * D) * sizeof(KV);
+        store_vals<KV>(dst + j0 * sizeof(KV), lo, V);
+        store_vals<KV>(dst + (j0 + half) * sizeof(KV), hi, V);
+      }
+    } else {
+      int uu = u - k_items;
+      int h = uu / dv, j0 = (uu - h * dv) * V;
+      const char* src = reinterpret_cast<const char*>(a.v) + (tok * a.v_row_stride + (int64_t)h * D + j0) * sizeof(T);
+      float x[V];
+      Elem<T>::load(src, x);
+      char* dst = reinterpret_cast<char*>(a.v_cache) + (slot * a.cache_slot_stride + (int64_t)h * D + j0) * sizeof(KV);
+      store_vals<KV>(dst, x, V);
+    }
+  }
+}
+
+hipError_t launch_rope_kv_write(const RopeKVWriteArgs& a, hipStream_t stream) {
+  const int V = a.dtype == kF32 ? 4 : 8;
+  const int64_t per_tok = (a.k ? (int64_t)a.num_kv_heads * (a.head_dim / 2 / V + a.head_dim / V) : 0) +
+                          (a.q_out ? (int64_t)a.num_q_heads * (a.head_dim / 2 / V) : 0);
+  int64_t total = a.num_tokens * per_tok;
+  if (total == 0) return hipSuccess;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  dim3 grid((unsigned)blocks), block(256);
+  if (a.dtype == kBF16 && a.kv_dtype == kBF16)
+    hipLaunchKernelGGL((rope_kv_write_kernel<__bf16, __bf16>), grid, block, 0, stream, a);
+  else if (a.dtype == kF32 && a.kv_dtype == kF32)
+    hipLaunchKernelGGL((rope_kv_write_kernel<float, float>), grid, block, 0, stream, a);
+  else if (a.dtype == kF32 && a.kv_dtype == kBF16)
+    hipLaunchKernelGGL((rope_kv_write_kernel<float, __bf16>), grid, block, 0, stream, a);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+}  // namespace gllm

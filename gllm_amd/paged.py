@@ -1,0 +1,216 @@
+"""Python entry points over the C ABI: fused RoPE + KV write, batch plans and
+paged attention.  Tensors are torch device tensors; every call is enqueued on
+torch's current stream of the tensors' device.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+
+
+def _rows(t: torch.Tensor, heads: int, head_dim: int, name: str) -> int:
+    """Row stride (elements) of a [..., heads, head_dim] tensor whose leading
+    dims flatten to rows without a copy."""
+    if t.dim() < 2 or t.shape[-1] != head_dim or t.shape[-2] != heads:
+        raise ValueError(f"{name}: expected [..., {heads}, {head_dim}], got {tuple(t.shape)}")
+    if t.stride(-1) != 1 or t.stride(-2) != head_dim:
+        raise ValueError(f"{name}: head dim and heads must be contiguous")
+    lead = t.shape[:-2]
+    stride = t.stride(-3) if t.dim() >= 3 else heads * head_dim
+    # leading dims must flatten to one row axis of constant stride
+    expect = stride
+    for d in range(t.dim() - 3, -1, -1):
+        if t.shape[d] > 1 and t.stride(d) != expect:
+            raise ValueError(f"{name}: leading dims do not flatten to rows")
+        expect *= t.shape[d]
+    del lead
+    return stride
+
+
+def rope_kv_write(k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                  k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                  query_lens: torch.Tensor | None = None, q: torch.Tensor | None = None,
+                  q_out: torch.Tensor | None = None, rope_rows: torch.Tensor | None = None) -> None:
+    """RoPE on k (and q -> q_out) plus the KV-cache write of
+    ``gllm/model/layers/attention.py:151-161``.
+
+    k/v ``[..., Hkv, D]`` (token rows), cos/sin ``[..., D/2]`` with one row per
+    token (or ``rope_rows`` indexing a table), caches ``[num_slots, Hkv, D]``,
+    ``slot_mapping`` int64 with one slot per token.  With ``query_lens``
+    (padded ``[B, T_q]`` token layout) rows past each sequence's length are not
+    written.
+    """
+    Hkv, D = k.shape[-2], k.shape[-1]
+    if k.shape != v.shape:
+        raise ValueError("k and v shapes differ")
+    ks = _rows(k, Hkv, D, "k")
+    vs = _rows(v, Hkv, D, "v")
+    n = k.numel() // (Hkv * D)
+    for t, nm in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        if t.dim() != 3 or t.shape[1:] != (Hkv, D) or t.stride(2) != 1 or t.stride(1) != D:
+            raise ValueError(f"{nm}: expected [num_slots, {Hkv}, {D}] with contiguous rows")
+    if k_cache.stride(0) != v_cache.stride(0) or k_cache.shape[0] != v_cache.shape[0]:
+        raise ValueError("k_cache and v_cache must have the same shape and slot stride")
+    sm = slot_mapping.reshape(-1)
+    if sm.dtype != torch.int64 or sm.numel() != n or not sm.is_contiguous():
+        raise ValueError("slot_mapping must be contiguous int64 with one entry per token")
+    cs = cos.reshape(-1, cos.shape[-1])
+    sn = sin.reshape(-1, sin.shape[-1])
+    if cs.stride(-1) != 1 or sn.stride(-1) != 1 or cs.stride(0) != sn.stride(0):
+        raise ValueError("cos/sin must have contiguous rows of equal stride")
+    if cs.dtype != k.dtype or sn.dtype != k.dtype:
+        raise ValueError("cos/sin must be in the model dtype")
+    if cs.shape[-1] < D // 2 or (rope_rows is None and cs.shape[0] < n):
+        raise ValueError("cos/sin need one row of at least D/2 entries per token")
+    tps = 0
+    ql = None
+    if query_lens is not None:
+        ql = query_lens.to(torch.int32).contiguous()
+        tps = n // ql.numel()
+    qs = qos = 0
+    Hq = 1
+    if q_out is not None:
+        Hq = q.shape[-2]
+        qs = _rows(q, Hq, D, "q")
+        qos = _rows(q_out, Hq, D, "q_out")
+    rr = None
+    if rope_rows is not None:
+        rr = rope_rows.reshape(-1).to(torch.int64).contiguous()
+    dev = k.device
+    lib = _lib.load()
+    _lib.check(lib.gllm_rope_kv_write(
+        _lib.ptr(q), _lib.ptr(q_out), k.data_ptr(), v.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+        sm.data_ptr(), _lib.ptr(ql), tps, cs.data_ptr(), sn.data_ptr(), _lib.ptr(rr), cs.stride(0), n,
+        Hq, Hkv, D, qs, ks, vs, qos, k_cache.stride(0), k_cache.shape[0],
+        _lib.dtype_code(k.dtype), _lib.dtype_code(k_cache.dtype), _lib.stream_ptr(dev)))
+
+
+def rope_rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                rope_rows: torch.Tensor | None = None) -> torch.Tensor:
+    """Rotate-half RoPE of ``x [..., H, D]`` (``attention.py:91-118``),
+    bit-identical to the reference's per-op rounding; returns a new tensor."""
+    H, D = x.shape[-2], x.shape[-1]
+    xs = _rows(x, H, D, "x")
+    out = torch.empty_like(x, memory_format=torch.contiguous_format)
+    n = x.numel() // (H * D)
+    cs = cos.reshape(-1, cos.shape[-1])
+    sn = sin.reshape(-1, sin.shape[-1])
+    rr = None if rope_rows is None else rope_rows.reshape(-1).to(torch.int64).contiguous()
+    if cs.shape[-1] < D // 2 or (rr is None and cs.shape[0] < n) or cs.stride(0) != sn.stride(0):
+        raise ValueError("cos/sin need one row of at least D/2 entries per token")
+    lib = _lib.load()
+    _lib.check(lib.gllm_rope_kv_write(
+        x.data_ptr(), out.data_ptr(), None, None, None, None, None, None, 0, cs.data_ptr(), sn.data_ptr(),
+        _lib.ptr(rr), cs.stride(0), n, H, 1, D, xs, 0, 0, H * D, 0, 0,
+        _lib.dtype_code(x.dtype), _lib.dtype_code(x.dtype), _lib.stream_ptr(x.device)))
+    return out
+
+
+class AttentionPlan:
+    """Work plan for one batch (built once per engine step, reused by every
+    layer).  Lengths are host ints, as ``gllm/llm/llm.py:233-241`` has them.
+
+    ``q_seq_stride`` > 0: sequence i's rows start at ``i * q_seq_stride`` (the
+    reference's padded ``[B, T_q]`` layout); 0: packed rows.
+    """
+
+    def __init__(self, query_lens, seq_lens, *, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                 block_size: int, dtype: torch.dtype, device, q_seq_stride: int = 0,
+                 split_tokens: int = 0):
+        ql = [int(x) for x in query_lens]
+        sl = [int(x) for x in seq_lens]
+        if len(ql) != len(sl):
+            raise ValueError("query_lens and seq_lens differ in length")
+        lib = _lib.load()
+        self._lib = lib
+        self._h = ctypes.c_void_p()
+        qa = (ctypes.c_int32 * max(len(ql), 1))(*ql)
+        sa = (ctypes.c_int32 * max(len(sl), 1))(*sl)
+        _lib.check(lib.gllm_attn_plan_create(ctypes.byref(self._h), qa, sa, len(ql), q_seq_stride,
+                                             num_q_heads, num_kv_heads, head_dim, block_size,
+                                             _lib.dtype_code(dtype), split_tokens))
+        self.num_q_heads, self.num_kv_heads, self.head_dim = num_q_heads, num_kv_heads, head_dim
+        self.block_size, self.dtype = block_size, dtype
+        self.query_lens, self.seq_lens = ql, sl
+        self.q_seq_stride = q_seq_stride
+        self.device = torch.device(device)
+        nbytes = lib.gllm_attn_plan_workspace_bytes(self._h)
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        _lib.check(lib.gllm_attn_plan_upload(self._h, self.workspace.data_ptr(), nbytes,
+                                             _lib.stream_ptr(self.device)))
+
+    @property
+    def info(self) -> dict:
+        arr = (ctypes.c_int64 * 6)()
+        _lib.check(self._lib.gllm_attn_plan_info(self._h, arr, 6))
+        keys = ("work_items", "split_tokens", "decode_seqs", "prefill_seqs", "partials", "rows")
+        return dict(zip(keys, list(arr)))
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            self._lib.gllm_attn_plan_destroy(h)
+            self._h = ctypes.c_void_p()
+
+
+def paged_attention(plan: AttentionPlan, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                    block_table: torch.Tensor, out: torch.Tensor | None = None,
+                    rope: tuple | None = None, scale: float | None = None) -> torch.Tensor:
+    """Attention over the paged cache for every query row in ``plan``.
+
+    q ``[rows, Hq, D]`` or ``[B, T_q, Hq, D]`` (rows flattened), caches
+    ``[num_slots, Hkv, D]``, block_table int32 ``[B, W]``.  ``rope`` =
+    ``(cos, sin, mode)`` with mode ``"position"`` (table rows ``c_i + r``) or
+    ``"row"`` (one cos/sin row per query row, the reference's gathered
+    ``cos_pos``) rotates q on load.  Returns ``out`` (same layout as q).
+    """
+    Hq, Hkv, D = plan.num_q_heads, plan.num_kv_heads, plan.head_dim
+    qs = _rows(q, Hq, D, "q")
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    os_ = _rows(out, Hq, D, "out")
+    if q.dtype != plan.dtype or out.dtype != plan.dtype:
+        raise ValueError("q/out dtype differs from the plan's")
+    for t, nm in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        if t.dim() != 3 or t.shape[1:] != (Hkv, D) or t.stride(2) != 1 or t.stride(1) != D:
+            raise ValueError(f"{nm}: expected [num_slots, {Hkv}, {D}] with contiguous rows")
+    if k_cache.stride(0) != v_cache.stride(0):
+        raise ValueError("k_cache and v_cache slot strides differ")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(1) != 1:
+        raise ValueError("block_table must be int32 [B, W] with contiguous rows")
+    if block_table.shape[0] < len(plan.query_lens):
+        raise ValueError("block_table has fewer rows than the plan's sequences")
+    need = max((-(-s // plan.block_size) for s in plan.seq_lens), default=0)
+    if block_table.shape[1] < need:
+        raise ValueError(f"block_table width {block_table.shape[1]} < {need} blocks the longest sequence needs")
+    rows = q.numel() // (Hq * D)
+    if rows < plan.info["rows"]:
+        raise ValueError(f"q has {rows} rows, the plan addresses {plan.info['rows']}")
+    cos_p = sin_p = None
+    rs = 0
+    mode = _lib.ROPE_NONE
+    if rope is not None:
+        cos, sin, m = rope
+        mode = {"position": _lib.ROPE_BY_POSITION, "row": _lib.ROPE_BY_ROW}[m]
+        cos = cos.reshape(-1, cos.shape[-1])
+        sin = sin.reshape(-1, sin.shape[-1])
+        if cos.stride(-1) != 1 or sin.stride(-1) != 1 or cos.stride(0) != sin.stride(0):
+            raise ValueError("cos/sin must have contiguous rows of equal stride")
+        if cos.dtype != q.dtype:
+            raise ValueError("cos/sin must be in the model dtype")
+        need_rows = max(plan.seq_lens) if m == "position" else plan.info["rows"]
+        if cos.shape[0] < need_rows or cos.shape[1] < D // 2:
+            raise ValueError(f"cos/sin have {cos.shape[0]} rows, {need_rows} needed")
+        cos_p, sin_p, rs = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
+    sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    num_blocks = k_cache.shape[0] // plan.block_size
+    lib = _lib.load()
+    _lib.check(lib.gllm_paged_attention(
+        plan._h, q.data_ptr(), qs, out.data_ptr(), os_, k_cache.data_ptr(), v_cache.data_ptr(),
+        k_cache.stride(0), num_blocks, block_table.data_ptr(), block_table.stride(0), cos_p, sin_p, rs, mode,
+        sc, _lib.dtype_code(q.dtype), _lib.dtype_code(k_cache.dtype), _lib.stream_ptr(q.device)))
+    return out

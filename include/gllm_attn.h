@@ -1,0 +1,144 @@
+/*
+ * gllm_attn — MI355X (gfx950) attention hot path for gLLM, C ABI.
+ *
+ * Drop-in boundary for the attention path of TheEpicDolphin/gllm.  The
+ * reference is pure Python and binds no FFI; these entry points are what its
+ * call sites would bind (through ctypes):
+ *
+ *   gllm_rope_kv_write    replaces gllm/model/layers/attention.py:151-161
+ *                         (Attention.apply_rope :76-119 on k [and q], then the
+ *                         index_put_ of k/v through query_slot_mapping)
+ *   gllm_paged_attention  replaces gllm/model/layers/attention.py:163-178
+ *                         (the dense KV gather through slot_mapping plus
+ *                         reference_attention with the 0/-inf bias of
+ *                         gllm/llm/llm.py:249-274) for decode, prefill and
+ *                         mixed batches; q rotation may be fused in
+ *   gllm_attention_dense  replaces gllm/ops/attention/reference_attention.py:5-51
+ *                         and flash_attention.py:155-192 (same contract:
+ *                         q[B,T_q,Hq,D], k/v[B,T,Hkv,D], bias[B,T_q,T])
+ *   gllm_attn_plan_*      host-side work planning for one batch (the lengths
+ *                         gllm/llm/llm.py:233-241 derives), built once per
+ *                         engine step and reused by every layer
+ *
+ * Conventions: every data pointer is a device pointer the caller owns; the
+ * library never allocates device memory (the paged path uses a caller-sized
+ * workspace).  `stream` is a hipStream_t (NULL = default stream).  Every
+ * function returns GLLM_ATTN_OK or an error code and records a message for
+ * gllm_attn_last_error() (thread-local).  Strides are in elements.
+ */
+#ifndef GLLM_ATTN_H_
+#define GLLM_ATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  GLLM_ATTN_OK = 0,
+  GLLM_ATTN_EINVAL = 1,       /* bad argument (shape, stride, null pointer) */
+  GLLM_ATTN_EUNSUPPORTED = 2, /* valid but not implemented (dtype, head_dim) */
+  GLLM_ATTN_EHIP = 3          /* HIP runtime error */
+};
+
+enum { GLLM_DTYPE_F32 = 0, GLLM_DTYPE_BF16 = 1 };
+
+enum {
+  GLLM_ROPE_NONE = 0,        /* q already rotated */
+  GLLM_ROPE_BY_POSITION = 1, /* cos/sin table row = c_i + r (model.py:117-128 table) */
+  GLLM_ROPE_BY_ROW = 2       /* cos/sin row = query row index (model.py:195-196 gathered cos_pos) */
+};
+
+typedef struct gllm_attn_plan gllm_attn_plan;
+
+/* Thread-local message of the last failing call ("" if none). */
+const char* gllm_attn_last_error(void);
+int gllm_attn_version(void);
+
+/*
+ * Rotate k (and, if q_out != NULL, q) with rotate-half RoPE and write k/v rows
+ * into the paged cache.  Token t (0 <= t < num_tokens) writes slot
+ * slot_mapping[t] of k_cache / v_cache (each [num_slots, cache_slot_stride]).
+ * If query_lens != NULL, token t is row t % tokens_per_seq of sequence
+ * t / tokens_per_seq and rows past query_lens[seq] (the reference's padded
+ * rows, which it sends to dummy slot 0) are skipped.  Slots outside
+ * [0, num_slots) are never written.  cos/sin rows: rope_rows[t] if given,
+ * else t.  dtype is the model dtype of q/k/v/cos/sin; kv_dtype the cache's.
+ * Every op is rounded to the model dtype in the reference's order, so the
+ * written K/V are bit-identical to attention.py:151-161.  With k == v == NULL
+ * only q is rotated into q_out (Attention.apply_rope on one tensor).
+ */
+int gllm_rope_kv_write(const void* q, void* q_out, const void* k, const void* v,
+                       void* k_cache, void* v_cache, const int64_t* slot_mapping,
+                       const int32_t* query_lens, int64_t tokens_per_seq,
+                       const void* cos, const void* sin, const int64_t* rope_rows,
+                       int64_t rope_row_stride, int64_t num_tokens, int32_t num_q_heads,
+                       int32_t num_kv_heads, int32_t head_dim, int64_t q_row_stride,
+                       int64_t k_row_stride, int64_t v_row_stride, int64_t q_out_row_stride,
+                       int64_t cache_slot_stride, int64_t num_slots, int32_t dtype,
+                       int32_t kv_dtype, void* stream);
+
+/*
+ * Plan the work for one batch from HOST lengths.  Sequence i has
+ * query_lens[i] query rows starting at row i * q_seq_stride of q/out
+ * (q_seq_stride = the padded T_q of the reference's [B, T_q, ...] layout), or,
+ * if q_seq_stride == 0, packed rows (cumulative query_lens).  seq_lens[i] =
+ * context + query length, as llm.py:233-236.  split_tokens = context tokens
+ * per decode split (multiple of 32; 0 = choose from the batch and the CU
+ * count).  No device work happens here.
+ */
+int gllm_attn_plan_create(gllm_attn_plan** plan, const int32_t* query_lens,
+                          const int32_t* seq_lens, int32_t num_seqs, int64_t q_seq_stride,
+                          int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                          int32_t block_size, int32_t dtype, int32_t split_tokens);
+/* Device bytes the plan needs (work list, split partials, tickets). */
+size_t gllm_attn_plan_workspace_bytes(const gllm_attn_plan* plan);
+/* Stream-ordered upload of the plan into `workspace` (>= workspace_bytes).
+ * The workspace must stay alive and untouched while launches use the plan. */
+int gllm_attn_plan_upload(gllm_attn_plan* plan, void* workspace, size_t workspace_bytes, void* stream);
+/* Plan facts: [0] work items, [1] split length, [2] decode-path sequences,
+ * [3] prefill-path sequences, [4] split partials, [5] total query rows. */
+int gllm_attn_plan_info(const gllm_attn_plan* plan, int64_t* info, int32_t n);
+int gllm_attn_plan_destroy(gllm_attn_plan* plan);
+
+/*
+ * Paged attention for every query row the plan describes.  q/out rows are
+ * [rows, num_q_heads * head_dim] with row strides in elements (heads at
+ * h * head_dim, head dim contiguous).  k_cache/v_cache: [num_blocks *
+ * block_size, cache_slot_stride] (one layer of the reference's
+ * [2, L, NB, bs, Hkv, D] pool).  block_table: int32 rows of
+ * block_table_stride, row i covering sequence i's ceil(seq_len / bs) blocks.
+ * Key p of sequence i is visible to query row r iff p <= c_i + r.
+ * Query head h reads kv head h / (num_q_heads / num_kv_heads).
+ * rope_mode != NONE rotates q on load (bit-identical to apply_rope).
+ * bf16/bf16 runs the MFMA kernels (head_dim 64 or 128); f32 model dtype runs
+ * the fp32 kernel (kv f32 or bf16).  Returns after enqueueing on `stream`.
+ */
+int gllm_paged_attention(const gllm_attn_plan* plan, const void* q, int64_t q_row_stride,
+                         void* out, int64_t out_row_stride, const void* k_cache,
+                         const void* v_cache, int64_t cache_slot_stride, int64_t num_blocks,
+                         const int32_t* block_table, int64_t block_table_stride,
+                         const void* rope_cos, const void* rope_sin, int64_t rope_row_stride,
+                         int32_t rope_mode, float scale, int32_t dtype, int32_t kv_dtype,
+                         void* stream);
+
+/*
+ * reference_attention(q, k, v, bias): softmax(q k^T * scale + bias) v with
+ * GQA.  q/out [B, T_q, Hq, D] (row stride q_row_stride, batch = T_q rows),
+ * k/v [B, T, Hkv, D] with the given batch / row strides, bias [B, T_q, T]
+ * (model dtype) with batch / row strides, last dim contiguous.  A row whose
+ * bias is -inf everywhere comes out NaN, as torch's softmax makes it.
+ */
+int gllm_attention_dense(const void* q, int64_t q_row_stride, const void* k, int64_t k_batch_stride,
+                         int64_t k_row_stride, const void* v, int64_t v_batch_stride,
+                         int64_t v_row_stride, const void* bias, int64_t bias_batch_stride,
+                         int64_t bias_row_stride, void* out, int64_t out_row_stride, int32_t batch,
+                         int32_t q_len, int32_t kv_len, int32_t num_q_heads, int32_t num_kv_heads,
+                         int32_t head_dim, float scale, int32_t dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GLLM_ATTN_H_ */

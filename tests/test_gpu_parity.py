@@ -1,0 +1,262 @@
+"""GPU parity of the HIP kernels against the CPU oracle (identical seeded
+inputs).  Bar: bit-exact for the RoPE/KV-write indexing and values; bf16
+attention outputs within max-abs 2e-2 and mean-abs 2e-3 of the fp32 oracle;
+fp32 outputs within 1e-4."""
+import math
+
+import pytest
+import torch
+
+import gllm_amd
+from gllm_amd import paged
+from oracle import attention as oa
+from oracle import metadata as om
+from oracle import rope as orope
+from tests.gpu_helpers import assert_close_bf16, make_batch, oracle_paged
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _bits(t):
+    return t.cpu().contiguous().view(torch.int16 if t.element_size() == 2 else torch.int32)
+
+
+# ------------------------------------------------------------ (a) RoPE + KV write
+@pytest.mark.parametrize("dtype,kv_dtype,D", [(torch.bfloat16, torch.bfloat16, 64),
+                                              (torch.bfloat16, torch.bfloat16, 128),
+                                              (torch.float32, torch.float32, 64),
+                                              (torch.float32, torch.bfloat16, 128)])
+def test_rope_kv_write_bit_exact(dtype, kv_dtype, D):
+    print(f"rope_kv_write dtype={dtype} kv={kv_dtype} D={D}", flush=True)
+    g = torch.Generator().manual_seed(10 + D)
+    ctx = [0, 17, 40, 3]
+    ql = [9, 1, 24, 16]
+    Hq, Hkv, bs, nb = 8, 2, 16, 64
+    bt = om.random_block_tables([c + q for c, q in zip(ctx, ql)], bs, nb, g, width=8)
+    meta = om.build_metadata(ctx, ql, bt, bs, dtype)
+    B, Tq = meta.query_slot_mapping.shape
+    q = torch.randn(B, Tq, Hq, D, generator=g).to(dtype)
+    k = torch.randn(B, Tq, Hkv, D, generator=g).to(dtype)
+    v = torch.randn(B, Tq, Hkv, D, generator=g).to(dtype)
+    cos_t, sin_t = orope.rope_cache(128, D, 500000.0, dtype)
+    cos, sin = cos_t[meta.positions], sin_t[meta.positions]
+    sentinel_k = torch.randn(nb * bs, Hkv, D, generator=g).to(kv_dtype)
+    sentinel_v = torch.randn(nb * bs, Hkv, D, generator=g).to(kv_dtype)
+    # oracle: reference order (attention.py:151-161) on CPU
+    kc_ref, vc_ref = sentinel_k.clone(), sentinel_v.clone()
+    q_ref = orope.apply_rope(q, cos, sin)
+    k_ref = orope.apply_rope(k, cos, sin)
+    oa.kv_write(kc_ref, vc_ref, meta.query_slot_mapping, k_ref, v)
+    # product
+    kc, vc = sentinel_k.to(DEV), sentinel_v.to(DEV)
+    q_out = torch.empty(B, Tq, Hq, D, dtype=dtype, device=DEV)
+    paged.rope_kv_write(k.to(DEV), v.to(DEV), cos.to(DEV), sin.to(DEV), kc, vc,
+                        meta.query_slot_mapping.to(DEV), query_lens=meta.query_lens.to(DEV),
+                        q=q.to(DEV), q_out=q_out)
+    torch.cuda.synchronize()
+    # block 0 is the dummy the reference's padded rows write; everything else bit-exact
+    assert torch.equal(_bits(kc)[bs:], _bits(kc_ref)[bs:])
+    assert torch.equal(_bits(vc)[bs:], _bits(vc_ref)[bs:])
+    assert torch.equal(_bits(kc)[:bs], _bits(sentinel_k)[:bs])  # padded rows skipped
+    for i in range(B):
+        assert torch.equal(_bits(q_out[i, :ql[i]]), _bits(q_ref[i, :ql[i]]))
+    # apply_rope drop-in on a whole tensor
+    qr = paged.rope_rotate(q.to(DEV), cos.to(DEV), sin.to(DEV))
+    assert torch.equal(_bits(qr), _bits(q_ref))
+
+
+# ------------------------------------------------------------ (b) decode
+@pytest.mark.parametrize("Hq,Hkv,D", [(32, 8, 64), (32, 8, 128), (64, 8, 128), (8, 8, 64), (16, 1, 64)])
+@pytest.mark.parametrize("split", [0, 32, 96])
+def test_decode_parity(Hq, Hkv, D, split):
+    print(f"decode Hq={Hq} Hkv={Hkv} D={D} split={split}", flush=True)
+    lens = [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 100, 255, 256, 257, 700, 1025]
+    b = make_batch([L - 1 for L in lens], [1] * len(lens), Hq, Hkv, D)
+    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D,
+                               block_size=16, dtype=torch.bfloat16, device=DEV, split_tokens=split)
+    ref = oracle_paged(b)
+    for rep in range(2):  # second launch checks the split tickets were reset
+        out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
+        torch.cuda.synchronize()
+        assert_close_bf16(out, ref, f"decode rep {rep}")
+
+
+def test_decode_multi_query_rows():
+    """q_len * G <= 16 stays on the decode path with a causal mask inside it."""
+    print("decode multi-query", flush=True)
+    b = make_batch([40, 0, 200, 7], [4, 3, 2, 4], 16, 4, 64)
+    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=16, num_kv_heads=4, head_dim=64,
+                               block_size=16, dtype=torch.bfloat16, device=DEV, split_tokens=64)
+    assert plan.info["decode_seqs"] == 4
+    out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
+    assert_close_bf16(out, oracle_paged(b), "decode multi-row")
+
+
+# ------------------------------------------------------------ (c) prefill
+@pytest.mark.parametrize("Hq,Hkv,D", [(32, 8, 128), (32, 8, 64), (8, 1, 64), (16, 16, 128), (64, 8, 128)])
+def test_prefill_parity(Hq, Hkv, D):
+    print(f"prefill Hq={Hq} Hkv={Hkv} D={D}", flush=True)
+    ctx = [0, 0, 0, 37, 300]
+    ql = [1 + 32, 130, 64, 77, 45]
+    b = make_batch(ctx, ql, Hq, Hkv, D)
+    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D,
+                               block_size=16, dtype=torch.bfloat16, device=DEV)
+    out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
+    torch.cuda.synchronize()
+    assert_close_bf16(out, oracle_paged(b), "prefill")
+
+
+def test_prefill_rope_in_kernel_matches_prerotated():
+    """RoPE fused into the attention kernel's q load == RoPE applied first."""
+    print("prefill rope fused", flush=True)
+    b = make_batch([0, 50], [100, 70], 32, 8, 128, theta=500000.0)
+    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=32, num_kv_heads=8, head_dim=128,
+                               block_size=16, dtype=torch.bfloat16, device=DEV)
+    pos = torch.cat([torch.arange(c, c + q) for c, q in zip(b.ctx_lens, b.q_lens)])
+    qr_ref = orope.apply_rope(b.q.cpu().unsqueeze(0), b.cos.cpu()[pos].unsqueeze(0),
+                              b.sin.cpu()[pos].unsqueeze(0))[0]
+    fused = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table,
+                                  rope=(b.cos, b.sin, "position"))
+    torch.cuda.synchronize()
+    assert_close_bf16(fused, oracle_paged(b, qr_ref), "prefill fused rope")
+    # decode path with rope by position too
+    d = make_batch([10, 500], [1, 1], 32, 8, 128, theta=500000.0)
+    dplan = paged.AttentionPlan(d.q_lens, d.seq_lens, num_q_heads=32, num_kv_heads=8, head_dim=128,
+                                block_size=16, dtype=torch.bfloat16, device=DEV)
+    pos = torch.tensor([10, 500])
+    qd = orope.apply_rope(d.q.cpu().unsqueeze(0), d.cos.cpu()[pos].unsqueeze(0), d.sin.cpu()[pos].unsqueeze(0))[0]
+    outd = paged.paged_attention(dplan, d.q, d.k_cache, d.v_cache, d.block_table, rope=(d.cos, d.sin, "position"))
+    assert_close_bf16(outd, oracle_paged(d, qd), "decode fused rope")
+
+
+# ------------------------------------------------------------ (d) mixed launch
+def test_mixed_batch_one_launch():
+    print("mixed", flush=True)
+    ctx = [100, 0, 2000, 513, 64, 1000]
+    ql = [1, 96, 1, 64, 1, 33]
+    b = make_batch(ctx, ql, 32, 8, 128)
+    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=32, num_kv_heads=8, head_dim=128,
+                               block_size=16, dtype=torch.bfloat16, device=DEV, split_tokens=256)
+    info = plan.info
+    assert info["decode_seqs"] == 3 and info["prefill_seqs"] == 3
+    out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
+    torch.cuda.synchronize()
+    assert_close_bf16(out, oracle_paged(b), "mixed")
+
+
+# ------------------------------------------------------------ fp32 path
+def test_fp32_paged_parity():
+    print("fp32 paged", flush=True)
+    b = make_batch([0, 30, 77], [20, 1, 5], 8, 2, 64, dtype=torch.float32)
+    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=8, num_kv_heads=2, head_dim=64,
+                               block_size=16, dtype=torch.float32, device=DEV)
+    out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
+    torch.cuda.synchronize()
+    d = (out.cpu() - oracle_paged(b)).abs().max().item()
+    assert d < 1e-4, d
+
+
+# ------------------------------------------------------------ dense-bias op
+@pytest.mark.parametrize("B,Tq,T,Hq,Hkv,D", [(1, 8, 8, 1, 1, 128), (1, 16, 16, 1, 1, 128), (1, 40, 40, 1, 1, 128),
+                                             (1, 256, 256, 1, 1, 128), (1, 32, 256, 1, 1, 128),
+                                             (1, 32, 256, 2, 1, 128), (8, 32, 256, 1, 1, 128),
+                                             (3, 5, 77, 32, 8, 64)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_dense_op_reference_shapes(B, Tq, T, Hq, Hkv, D, dtype):
+    """The reference's own op-test shapes (tests/test_attention_op.py:12-34),
+    causal-with-offset bias (:56-61), seeded."""
+    print(f"dense {B},{Tq},{T},{Hq},{Hkv},{D} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(B * 1000 + T + Hq)
+    q = torch.randn(B, Tq, Hq, D, generator=g).to(dtype)
+    k = torch.randn(B, T, Hkv, D, generator=g).to(dtype)
+    v = torch.randn(B, T, Hkv, D, generator=g).to(dtype)
+    bias = torch.zeros(B, Tq, T, dtype=dtype)
+    bias[:, :, T - Tq:] = torch.full((Tq, Tq), float("-inf")).triu(1).to(dtype)
+    ref = oa.reference_attention(q.float(), k.float(), v.float(), bias.float())
+    out = gllm_amd.reference_attention(q.to(DEV), k.to(DEV), v.to(DEV), bias.to(DEV))
+    torch.cuda.synchronize()
+    if dtype == torch.float32:
+        assert torch.allclose(out.cpu(), ref, rtol=1e-3, atol=1e-3)   # the reference test's bar
+        assert (out.cpu() - ref).abs().max().item() < 1e-4
+    else:
+        assert_close_bf16(out, ref, "dense bf16")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_dense_op_engine_bias_and_masked_rows(dtype):
+    """Left-padded engine bias (llm.py:259-274) and a fully masked row (NaN,
+    as torch's softmax)."""
+    print(f"dense engine bias {dtype}", flush=True)
+    g = torch.Generator().manual_seed(4)
+    ctx, ql = [5, 0, 60], [3, 9, 1]
+    bt = om.random_block_tables([c + x for c, x in zip(ctx, ql)], 16, 32, g)
+    meta = om.build_metadata(ctx, ql, bt, 16, dtype)
+    B, Tq, T = meta.bias.shape
+    q = torch.randn(B, Tq, 8, 64, generator=g).to(dtype)
+    k = torch.randn(B, T, 2, 64, generator=g).to(dtype)
+    v = torch.randn(B, T, 2, 64, generator=g).to(dtype)
+    bias = meta.bias.clone()
+    bias[1, 4, :] = float("-inf")
+    ref = oa.reference_attention(q.float(), k.float(), v.float(), bias.float())
+    out = gllm_amd.reference_attention(q.to(DEV), k.to(DEV), v.to(DEV), bias.to(DEV)).cpu().float()
+    assert torch.isnan(out[1, 4]).all() and torch.isnan(ref[1, 4]).all()
+    fin = torch.isfinite(ref)
+    d = (out[fin] - ref[fin]).abs()
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert d.max().item() < tol
+
+
+# ------------------------------------------------------------ call-site drop-in
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_attention_forward_dropin(dtype):
+    """gllm_amd.Attention.attention == attention.py:151-178 (oracle) on real
+    rows; cache contents bit-exact outside the dummy block."""
+    print(f"attention drop-in {dtype}", flush=True)
+    g = torch.Generator().manual_seed(21)
+    Hq, Hkv, D, bs, nb = 32, 8, 64, 16, 64
+    ctx, ql = [0, 33, 100, 7], [12, 1, 1, 20]
+    bt = om.random_block_tables([c + x for c, x in zip(ctx, ql)], bs, nb, g, width=16)
+    meta = om.build_metadata(ctx, ql, bt, bs, dtype)
+    B, Tq = meta.query_slot_mapping.shape
+    q = torch.randn(B, Tq, Hq, D, generator=g).to(dtype)
+    k = torch.randn(B, Tq, Hkv, D, generator=g).to(dtype)
+    v = torch.randn(B, Tq, Hkv, D, generator=g).to(dtype)
+    cos_t, sin_t = orope.rope_cache(256, D, 500000.0, dtype)
+    cos, sin = cos_t[meta.positions], sin_t[meta.positions]
+    kv = torch.randn(2, nb * bs, Hkv, D, generator=g).to(dtype)
+    kv_ref = kv.clone()
+    ref, _, _ = oa.attention_layer_forward(q, k, v, cos, sin, kv_ref[0], kv_ref[1], meta, sdpa_dtype=torch.float32)
+
+    class Cfg:
+        num_attn_heads, num_kv_heads, head_dim, hidden_size = Hq, Hkv, D, Hq * D
+
+    Cfg.dtype = dtype
+    w = {f"model.layers.0.self_attn.{n}_proj.weight": torch.zeros(1) for n in "qkvo"}
+    att = gllm_amd.Attention(0, Cfg, w)
+    gm = gllm_amd.AttentionMetadata(
+        query_lens=meta.query_lens.to(DEV), seq_lens=meta.seq_lens.to(DEV), max_seq_len=meta.max_seq_len,
+        block_table=meta.block_table.to(DEV), slot_mapping=meta.slot_mapping.to(DEV),
+        query_slot_mapping=meta.query_slot_mapping.to(DEV), bias=None, block_size=bs)
+    kvd = kv.to(DEV)
+    out = att.attention(q.to(DEV), k.to(DEV), v.to(DEV), cos.to(DEV), sin.to(DEV), kvd, gm).cpu()
+    assert torch.equal(_bits(kvd)[:, bs:], _bits(kv_ref)[:, bs:])
+    for i in range(B):
+        if dtype == torch.float32:
+            assert (out[i, :ql[i]] - ref[i, :ql[i]]).abs().max().item() < 1e-4
+        else:
+            assert_close_bf16(out[i, :ql[i]], ref[i, :ql[i]], f"drop-in seq {i}")
+
+
+# ------------------------------------------------------------ errors
+def test_errors_are_raised():
+    print("errors", flush=True)
+    with pytest.raises(NotImplementedError):
+        paged.AttentionPlan([1], [10], num_q_heads=8, num_kv_heads=2, head_dim=96, block_size=16,
+                            dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):
+        paged.AttentionPlan([5], [3], num_q_heads=8, num_kv_heads=2, head_dim=64, block_size=16,
+                            dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(AssertionError):
+        gllm_amd.reference_attention(torch.zeros(1, 1, 1, 64, device=DEV), torch.zeros(1, 2, 1, 64, device=DEV),
+                                     torch.zeros(1, 3, 1, 64, device=DEV), torch.zeros(1, 1, 2, device=DEV))

@@ -1,0 +1,261 @@
+"""Pins the CPU oracle against closed forms, brute force and invariants.
+
+The reference ships no golden vectors for this path, so each oracle function
+is checked here against what the mathematics fixes, chosen so that a plausible
+slip (wrong half pairing, wrong GQA index, dropped scale, off-by-one in the
+mask, wrong padding side) fails at least one test.
+"""
+import itertools
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from oracle import bruteforce as bf
+from oracle import metadata as om
+from oracle import rope as orope
+
+
+# ---------------------------------------------------------------- metadata
+def _tiny_batch(seed, B=3, bs=4, nb=40):
+    g = torch.Generator().manual_seed(seed)
+    ctx = torch.randint(0, 9, (B,), generator=g).tolist()
+    q = torch.randint(1, 6, (B,), generator=g).tolist()
+    bt = om.random_block_tables([c + n for c, n in zip(ctx, q)], bs, nb, g, width=8)
+    return ctx, q, bt, bs
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_metadata_bruteforce(seed):
+    ctx, q, bt, bs = _tiny_batch(seed)
+    m = om.build_metadata(ctx, q, bt, bs)
+    B = len(q)
+    max_ctx, max_q = max(ctx), max(q)
+    T = max_ctx + max_q
+    assert m.slot_mapping.shape == (B, T) and m.bias.shape == (B, max_q, T)
+    for i in range(B):
+        pad = max_ctx - ctx[i]
+        L = ctx[i] + q[i]
+        for j in range(T):
+            p = j - pad
+            want_slot = om.slot_of(bt[i], p, bs) if 0 <= p < L else 0
+            assert int(m.slot_mapping[i, j]) == want_slot
+            for r in range(max_q):
+                # element-wise restatement of llm.py:264-274
+                if j < pad:
+                    want = -math.inf
+                elif j < max_ctx:
+                    want = 0.0
+                else:
+                    want = 0.0 if (j - max_ctx) <= r else -math.inf
+                assert float(m.bias[i, r, j]) == want
+                # mask-equivalence theorem on real rows: visible <=> p <= c+r
+                if r < q[i] and 0 <= p < L:
+                    assert (want == 0.0) == (p <= ctx[i] + r)
+                if r < q[i] and not (0 <= p < L):
+                    assert want == -math.inf
+        for r in range(max_q):
+            assert int(m.positions[i, r]) == ctx[i] + r
+            want = om.slot_of(bt[i], ctx[i] + r, bs) if r < q[i] else 0
+            assert int(m.query_slot_mapping[i, r]) == want
+
+
+def test_metadata_invariants():
+    g = torch.Generator().manual_seed(11)
+    lens = torch.randint(1, 200, (16,), generator=g).tolist()
+    bt = om.random_block_tables(lens, 16, 1024, g)
+    m = om.build_metadata([L - 1 for L in lens], [1] * 16, bt, 16)
+    live = [int(m.slot_mapping[i, j]) for i in range(16) for j in range(m.slot_mapping.shape[1])
+            if float(m.bias[i, 0, j]) == 0.0]
+    assert len(live) == len(set(live)) == sum(lens)
+    assert all(16 <= s < 1024 * 16 for s in live)       # block 0 never live
+    assert m.query_slot_mapping.shape == (16, 1)
+
+
+def test_allocator_semantics():
+    a = om.BlockAllocator(6)
+    assert a.reserve(2) == [5, 4]
+    a.release([5])
+    assert a.reserve(3) == [3, 2, 1]
+    assert 5 in a.cached
+    with pytest.raises(TypeError):
+        a.reserve(1)        # free list empty: dict.pop() without a key raises, as the reference
+    assert om.num_required_blocks(16, 16) == 1 and om.num_required_blocks(17, 16) == 2
+
+
+# ---------------------------------------------------------------- RoPE
+def test_rope_table_closed_form():
+    cos, sin = orope.rope_cache(64, 64, 500000.0, torch.float32)
+    assert torch.equal(cos[0], torch.ones(32)) and torch.equal(sin[0], torch.zeros(32))
+    for p in (1, 7, 63):
+        for j in (0, 5, 31):
+            a = p * 500000.0 ** (-2 * j / 64)
+            assert abs(float(cos[p, j]) - math.cos(a)) < 1e-5
+            assert abs(float(sin[p, j]) - math.sin(a)) < 1e-5
+    cb, sb = orope.rope_cache(64, 64, 500000.0, torch.bfloat16)
+    assert torch.equal(cb, cos.to(torch.bfloat16)) and torch.equal(sb, sin.to(torch.bfloat16))
+
+
+def test_rope_known_answers():
+    D = 8
+    x = torch.zeros(1, 1, 1, D)
+    x[..., 0] = 1.0                                   # pair (x_0, x_4) = (1, 0)
+    c = torch.zeros(1, 1, D // 2)
+    s = torch.zeros(1, 1, D // 2)
+    c[..., 0], s[..., 0] = 0.0, 1.0                   # 90 degrees
+    out = orope.apply_rope(x, c, s)
+    assert float(out[..., 0]) == 0.0 and float(out[..., 4]) == 1.0   # (1,0) -> (0,1)
+    x2 = torch.zeros(1, 1, 1, D)
+    x2[..., 4] = 1.0                                  # (0,1) -> (-1,0)
+    out2 = orope.apply_rope(x2, c, s)
+    assert float(out2[..., 0]) == -1.0 and float(out2[..., 4]) == 0.0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rope_properties(dtype):
+    g = torch.Generator().manual_seed(5)
+    D, theta = 64, 500000.0
+    cos, sin = orope.rope_cache(128, D, theta, dtype)
+    x = torch.randn(2, 5, 3, D, generator=g).to(dtype)
+    pos = torch.tensor([[0, 1, 2, 50, 127], [3, 9, 64, 100, 0]])
+    out = orope.apply_rope(x, cos[pos], sin[pos])
+    # position 0 is the identity, exactly
+    assert torch.equal(out[0, 0], x[0, 0]) and torch.equal(out[1, 4], x[1, 4])
+    # pair norms preserved; fp64 closed form agrees
+    tol = 1e-5 if dtype == torch.float32 else 3e-2
+    x64 = x.double()
+    o64 = out.double()
+    h = D // 2
+    n_in = x64[..., :h] ** 2 + x64[..., h:] ** 2
+    n_out = o64[..., :h] ** 2 + o64[..., h:] ** 2
+    assert torch.allclose(n_in, n_out, atol=tol * 10, rtol=tol * 10)
+    for b, t in itertools.product(range(2), range(5)):
+        ref = bf.rotate_fp64(x64[b, t].numpy(), int(pos[b, t]), theta)
+        assert np.allclose(o64[b, t].numpy(), ref, atol=tol * 4, rtol=tol)
+    if dtype == torch.float32:
+        # inverse rotation (sin -> -sin) recovers the input
+        back = orope.apply_rope(out, cos[pos], -sin[pos])
+        assert torch.allclose(back, x, atol=1e-5)
+
+
+# ---------------------------------------------------------------- attention op
+@pytest.mark.parametrize("B,Tq,T,Hq,Hkv,D", [(1, 3, 5, 1, 1, 4), (2, 2, 6, 4, 2, 8), (1, 4, 7, 8, 2, 4)])
+def test_reference_attention_bruteforce(B, Tq, T, Hq, Hkv, D):
+    g = torch.Generator().manual_seed(B * 100 + T)
+    q = torch.randn(B, Tq, Hq, D, generator=g)
+    k = torch.randn(B, T, Hkv, D, generator=g)
+    v = torch.randn(B, T, Hkv, D, generator=g)
+    bias = torch.zeros(B, Tq, T)
+    bias[:, :, T - Tq:] = torch.full((Tq, Tq), float("-inf")).triu(1)
+    bias[0, 0, 0] = float("-inf")
+    out = oa.reference_attention(q, k, v, bias)
+    ref = bf.sdpa_fp64(q.numpy(), k.numpy(), v.numpy(), bias.numpy())
+    assert np.allclose(out.numpy(), ref, atol=1e-5)
+
+
+def test_reference_attention_special_cases():
+    g = torch.Generator().manual_seed(1)
+    B, Tq, T, Hq, Hkv, D = 1, 2, 5, 4, 2, 8
+    q = torch.randn(B, Tq, Hq, D, generator=g)
+    k = torch.randn(B, T, Hkv, D, generator=g)
+    v = torch.randn(B, T, Hkv, D, generator=g)
+    one = torch.full((B, Tq, T), float("-inf"))
+    one[:, :, 3] = 0.0                               # exactly one visible key
+    out = oa.reference_attention(q, k, v, one)
+    for h in range(Hq):
+        assert torch.allclose(out[0, :, h], v[0, 3, h // 2].expand(Tq, D), atol=1e-6)
+    zq = torch.zeros_like(q)
+    bias = torch.zeros(B, Tq, T)
+    bias[:, :, 0] = float("-inf")
+    out = oa.reference_attention(zq, k, v, bias)   # Q = 0 => mean of visible V
+    for h in range(Hq):
+        assert torch.allclose(out[0, 0, h], v[0, 1:, h // 2].mean(0), atol=1e-6)
+    full = torch.full((B, Tq, T), float("-inf"))
+    assert torch.isnan(oa.reference_attention(q, k, v, full)).all()
+
+
+def test_gqa_head_mapping():
+    # kv head j carries constant value j in V; q head h must read h // G
+    B, Tq, T, Hq, Hkv, D = 1, 1, 3, 8, 2, 4
+    q = torch.randn(B, Tq, Hq, D)
+    k = torch.randn(B, T, Hkv, D)
+    v = torch.stack([torch.full((B, T, D), float(j)) for j in range(Hkv)], dim=2)
+    out = oa.reference_attention(q, k, v, torch.zeros(B, Tq, T))
+    for h in range(Hq):
+        assert torch.allclose(out[0, 0, h], torch.full((D,), float(h // 4)))
+
+
+# ---------------------------------------------------------------- call site
+def _layer_case(seed, dtype=torch.float32, bs=4):
+    g = torch.Generator().manual_seed(seed)
+    ctx, ql, bt, _ = _tiny_batch(seed, bs=bs)
+    Hq, Hkv, D = 4, 2, 8
+    meta = om.build_metadata(ctx, ql, bt, bs, dtype)
+    B, Tq = meta.query_slot_mapping.shape
+    nslots = 40 * bs
+    kc = torch.randn(nslots, Hkv, D, generator=g).to(dtype)
+    vc = torch.randn(nslots, Hkv, D, generator=g).to(dtype)
+    q = torch.randn(B, Tq, Hq, D, generator=g).to(dtype)
+    k = torch.randn(B, Tq, Hkv, D, generator=g).to(dtype)
+    v = torch.randn(B, Tq, Hkv, D, generator=g).to(dtype)
+    cos, sin = orope.rope_cache(64, D, 10000.0, dtype)
+    return ctx, ql, bt, meta, kc, vc, q, k, v, cos[meta.positions], sin[meta.positions]
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_layer_write_then_gather_and_paged_equivalence(seed):
+    ctx, ql, bt, meta, kc, vc, q, k, v, cos, sin = _layer_case(seed)
+    kc0, vc0 = kc.clone(), vc.clone()
+    out, qr, kr = oa.attention_layer_forward(q, k, v, cos, sin, kc, vc, meta)
+    B, Tq = meta.query_slot_mapping.shape
+    bs = 4
+    written = set()
+    for i in range(B):
+        for r in range(ql[i]):
+            s = int(meta.query_slot_mapping[i, r])
+            written.add(s)
+            assert torch.equal(kc[s], kr[i, r]) and torch.equal(vc[s], v[i, r])
+    # sentinel: everything outside written slots and dummy block 0 unchanged
+    for s in range(kc.shape[0]):
+        if s not in written and s >= bs:
+            assert torch.equal(kc[s], kc0[s]) and torch.equal(vc[s], vc0[s])
+    # the paged per-sequence form equals the dense padded form on real rows
+    rows = qr.reshape(B * Tq, *qr.shape[2:])
+    po = oa.paged_attention(rows, kc, vc, torch.from_numpy(bt), ctx, ql,
+                            [i * Tq for i in range(B)], bs)
+    for i in range(B):
+        assert torch.allclose(po[i * Tq:i * Tq + ql[i]], out[i, :ql[i]], atol=1e-5)
+
+
+def test_paged_attention_bruteforce():
+    ctx, ql, bt, meta, kc, vc, q, k, v, cos, sin = _layer_case(7)
+    B, Tq = meta.query_slot_mapping.shape
+    rows = q.reshape(B * Tq, *q.shape[2:])
+    po = oa.paged_attention(rows, kc, vc, torch.from_numpy(bt), ctx, ql, [i * Tq for i in range(B)], 4)
+    for i in range(B):
+        L = ctx[i] + ql[i]
+        slots = [om.slot_of(bt[i], p, 4) for p in range(L)]
+        kk = kc[slots].unsqueeze(0).numpy()
+        vv = vc[slots].unsqueeze(0).numpy()
+        qq = q[i:i + 1, :ql[i]].numpy()
+        bias = np.array([[0.0 if p <= ctx[i] + r else -np.inf for p in range(L)] for r in range(ql[i])])[None]
+        ref = bf.sdpa_fp64(qq, kk, vv, bias)
+        assert np.allclose(po[i * Tq:i * Tq + ql[i]].numpy(), ref[0], atol=1e-5)
+
+
+def test_lse_split_merge_identity():
+    g = torch.Generator().manual_seed(3)
+    s = torch.randn(4, 37, generator=g) * 3
+    v = torch.randn(37, 6, generator=g)
+    full = torch.softmax(s, -1) @ v
+    cuts = [0, 5, 17, 30, 37]
+    ms, ls, accs = [], [], []
+    for a, b in zip(cuts[:-1], cuts[1:]):
+        m = s[:, a:b].max(-1).values
+        e = torch.exp(s[:, a:b] - m.unsqueeze(-1))
+        ms.append(m)
+        ls.append(e.sum(-1))
+        accs.append(e @ v[a:b])
+    assert torch.allclose(oa.lse_merge(ms, ls, accs), full, atol=1e-6)
