@@ -31,7 +31,7 @@ SIGNATURES = {
     "gllm_rope_kv_write": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _i64, _i64,
                                           _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _p]),
     "gllm_attn_plan_create": (ctypes.c_int, [ctypes.POINTER(_p), _p, _p, _i32, _i64, _i32, _i32, _i32,
-                                             _i32, _i32, _i32]),
+                                             _i32, _i32, _i32, _i32]),
     "gllm_attn_plan_workspace_bytes": (_sz, [_p]),
     "gllm_attn_plan_upload": (ctypes.c_int, [_p, _p, _sz, _p]),
     "gllm_attn_plan_info": (ctypes.c_int, [_p, ctypes.POINTER(_i64), _i32]),

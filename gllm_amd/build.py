@@ -22,6 +22,8 @@ ARCH = "gfx950"
 
 SOURCES = ["api.hip", "rope_kv_write.hip", "paged_attention.hip", "attention_f32.hip"]
 NO_CONTRACT = {"rope_kv_write.hip", "attention_f32.hip"}
+# MFMA accumulators stay in VGPRs (no per-tile AGPR<->VGPR copies)
+EXTRA = {"paged_attention.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"]}
 COMMON = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     # packed fp32 VALU ops are disabled on purpose for every HIP unit
@@ -35,6 +37,7 @@ def _compile(src: str) -> str:
     cmd = [HIPCC, *COMMON, "-c", os.path.join(CSRC, src), "-o", obj]
     if src in NO_CONTRACT:
         cmd.insert(1, "-ffp-contract=off")
+    cmd[1:1] = EXTRA.get(src, [])
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr[-4000:]}")

@@ -53,7 +53,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 struct gllm_attn_plan {
   int32_t num_seqs = 0, Hq = 0, Hkv = 0, D = 0, bs = 0, dtype = 0;
   int32_t split_len = 0, max_q = 0;
-  int32_t n_decode_seqs = 0, n_prefill_seqs = 0;
+  int32_t n_decode_seqs = 0, n_prefill_seqs = 0, heads_per_wg = 8, decode_waves = 8;
   int64_t total_rows = 0;
   int64_t n_partials = 0;
   std::vector<SeqInfo> seqs;
@@ -115,7 +115,7 @@ int gllm_rope_kv_write(const void* q, void* q_out, const void* k, const void* v,
 int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const int32_t* seq_lens,
                           int32_t num_seqs, int64_t q_seq_stride, int32_t num_q_heads,
                           int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t dtype,
-                          int32_t split_tokens) {
+                          int32_t split_tokens, int32_t decode_heads_per_wg) {
   if (!out) return fail(GLLM_ATTN_EINVAL, "plan out-pointer is null");
   *out = nullptr;
   if (num_seqs < 0 || (num_seqs > 0 && (!query_lens || !seq_lens)))
@@ -133,6 +133,9 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
     return fail(GLLM_ATTN_EUNSUPPORTED, "dtype %d", dtype);
   }
   if (split_tokens < 0 || split_tokens % 32) return fail(GLLM_ATTN_EINVAL, "split_tokens must be a multiple of 32");
+  if (decode_heads_per_wg != 0 && decode_heads_per_wg != 1 && decode_heads_per_wg != 2 &&
+      decode_heads_per_wg != 4 && decode_heads_per_wg != 8)
+    return fail(GLLM_ATTN_EINVAL, "decode_heads_per_wg must be 0 (auto), 1, 2, 4 or 8");
   if (q_seq_stride < 0) return fail(GLLM_ATTN_EINVAL, "q_seq_stride < 0");
   const int G = num_q_heads / num_kv_heads;
 
@@ -168,22 +171,58 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
   }
 
   if (dtype == GLLM_DTYPE_BF16) {
-    // Split length: aim for ~16 decode waves per CU, in multiples of 32 keys.
     int cus = 256;
     int dev = 0;
     hipDeviceProp_t prop;
     if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0)
       cus = prop.multiProcessorCount;
-    int64_t S = split_tokens;
-    if (S == 0) {
-      const int64_t target = (int64_t)cus * 16;
-      S = (decode_tokens * num_kv_heads + target - 1) / std::max<int64_t>(target, 1);
-      S = std::min<int64_t>(std::max<int64_t>((S + 31) / 32 * 32, 128), 8192);
+    else
+      (void)hipGetLastError();
+    // Decode: one 8-wave workgroup per (sequence, split, HW kv heads); the
+    // other 8 / HW waves interleave each head's keys.  Rule (fitted to MI355X
+    // measurements of the benchmark batches): the first HW of 2, 1, 4, 8
+    // whose unsplit units give every CU its resident workgroups (2 at D=64,
+    // 1 at D=128) wins; HW=2 reads 256-byte runs of each slot and still
+    // spreads one sequence over several CUs.  If none fills the GPU, HW=2 and
+    // sequences are split into equal key ranges.  A split caches at most 511
+    // block ids.
+    int64_t cap = (int64_t)511 * block_size / 32 * 32;
+    cap = std::max<int64_t>(32, std::min<int64_t>(cap, 8192));
+    int64_t ndec = 0;
+    for (int i = 0; i < num_seqs; ++i)
+      if (query_lens[i] * G <= 16) ++ndec;
+    const int64_t target = (int64_t)cus * (head_dim == 64 ? 2 : 1);
+    int best_hw = 0;
+    const int hw_pref[4] = {2, 1, 4, 8};
+    for (int hw : hw_pref) {
+      if (decode_heads_per_wg && hw != decode_heads_per_wg) continue;
+      if (ndec * ((num_kv_heads + hw - 1) / hw) >= target) {
+        best_hw = hw;
+        break;
+      }
     }
+    const bool fills = best_hw != 0;
+    if (!fills) best_hw = decode_heads_per_wg ? decode_heads_per_wg : 2;
+    while (best_hw > 1 && best_hw / 2 >= num_kv_heads) best_hw /= 2;  // no idle head slots
+    const int best_nw = 8;
+    int64_t best_S = split_tokens;
+    if (best_S == 0) {
+      if (fills) {
+        best_S = cap;
+      } else {
+        const int64_t hg = (num_kv_heads + best_hw - 1) / best_hw;
+        best_S = (decode_tokens * hg + target - 1) / std::max<int64_t>(target, 1);
+        best_S = std::max<int64_t>((best_S + 31) / 32 * 32, 128);
+      }
+    }
+    best_S = std::min(best_S, cap);
+    p->heads_per_wg = best_hw;
+    p->decode_waves = best_nw;
+    const int hgroups = (num_kv_heads + best_hw - 1) / best_hw;
+    const int64_t S = best_S;
     p->split_len = (int32_t)S;
     struct Keyed { int64_t work; WorkItem it; };
     std::vector<Keyed> pf, dc;
-    const int kvg = (num_kv_heads + 3) / 4;
     for (int i = 0; i < num_seqs; ++i) {
       SeqInfo& s = p->seqs[i];
       const int L = s.ctx_len + s.q_len;
@@ -193,28 +232,37 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
         s.partial_base = (int32_t)p->n_partials;
         if (s.nsplits > 1) p->n_partials += (int64_t)num_kv_heads * s.nsplits;
         for (int sp = 0; sp < s.nsplits; ++sp)
-          for (int g4 = 0; g4 < kvg; ++g4) {
+          for (int hg = 0; hg < hgroups; ++hg) {
             const int64_t keys = std::min<int64_t>(L, (int64_t)(sp + 1) * S) - (int64_t)sp * S;
-            dc.push_back({keys, WorkItem{kItemDecode, i, sp, g4}});
+            dc.push_back({keys, WorkItem{kItemDecode | (hg << 8), i, sp, s.q_row_start, s.ctx_len, s.q_len,
+                                         s.nsplits, s.partial_base}});
           }
       } else {
         ++p->n_prefill_seqs;
         const int nrb = (s.q_len + 31) / 32;
-        const int nwg = (G * nrb + 3) / 4;
+        const int nwg = (G * nrb + 7) / 8;
         for (int h = 0; h < num_kv_heads; ++h)
           for (int w = 0; w < nwg; ++w) {
-            const int last_combo = std::min(w * 4 + 3, G * nrb - 1);
+            const int last_combo = std::min(w * 8 + 7, G * nrb - 1);
             const int64_t kend = s.ctx_len + std::min(s.q_len - 1, (last_combo / G) * 32 + 31) + 1;
-            pf.push_back({kend, WorkItem{kItemPrefill, i, h, w}});
+            pf.push_back({kend, WorkItem{kItemPrefill | (w << 8), i, h, s.q_row_start, s.ctx_len, s.q_len, 0, 0}});
           }
       }
     }
     // Longest work first so the tail is made of short items.
     std::stable_sort(pf.begin(), pf.end(), [](const Keyed& x, const Keyed& y) { return x.work > y.work; });
     std::stable_sort(dc.begin(), dc.end(), [](const Keyed& x, const Keyed& y) { return x.work > y.work; });
-    p->items.reserve(pf.size() + dc.size());
-    for (auto& k : pf) p->items.push_back(k.it);
-    for (auto& k : dc) p->items.push_back(k.it);
+    // Snake order: workgroups are dispatched slot-major (item k and item
+    // k + cus land on the same CU while every slot is free), so alternate the
+    // direction every `cus` items; each CU then pairs long work with short.
+    std::vector<Keyed> all;
+    all.reserve(pf.size() + dc.size());
+    for (auto& k : pf) all.push_back(k);
+    for (auto& k : dc) all.push_back(k);
+    for (size_t c0 = cus, chunk = 1; c0 < all.size(); c0 += cus, ++chunk)
+      if (chunk & 1) std::reverse(all.begin() + c0, all.begin() + std::min(all.size(), c0 + (size_t)cus));
+    p->items.reserve(all.size());
+    for (auto& k : all) p->items.push_back(k.it);
     if (p->items.size() > (size_t)INT32_MAX) {
       delete p;
       return fail(GLLM_ATTN_EINVAL, "too many work items");
@@ -252,9 +300,9 @@ size_t gllm_attn_plan_workspace_bytes(const gllm_attn_plan* p) { return p ? p->w
 
 int gllm_attn_plan_info(const gllm_attn_plan* p, int64_t* info, int32_t n) {
   if (!p || !info) return fail(GLLM_ATTN_EINVAL, "null plan or info");
-  const int64_t v[6] = {(int64_t)p->items.size(), p->split_len, p->n_decode_seqs, p->n_prefill_seqs,
-                        p->n_partials, p->total_rows};
-  for (int i = 0; i < n && i < 6; ++i) info[i] = v[i];
+  const int64_t v[8] = {(int64_t)p->items.size(), p->split_len, p->n_decode_seqs, p->n_prefill_seqs,
+                        p->n_partials, p->total_rows, p->heads_per_wg, p->decode_waves};
+  for (int i = 0; i < n && i < 8; ++i) info[i] = v[i];
   return ok();
 }
 
@@ -339,6 +387,9 @@ int gllm_paged_attention(const gllm_attn_plan* p, const void* q, int64_t q_row_s
   a.partial_ml = (float*)(p->ws + p->off_ml);
   a.partials = (float*)(p->ws + p->off_part);
   a.split_len = p->split_len;
+  a.n_partials = p->n_partials;
+  a.heads_per_wg = p->heads_per_wg;
+  a.decode_waves = p->decode_waves;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == GLLM_DTYPE_BF16)
     return hip_check(launch_paged_attention_bf16(a, p->n_prefill_seqs > 0, p->n_decode_seqs > 0, st),

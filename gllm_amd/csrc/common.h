@@ -38,11 +38,17 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return u >> 16;
 }
 
-__device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 
+// gfx950's v_cvt_pk_bf16_f32 rounds to nearest even, like torch's bf16 stores.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  bf16x2 r;
+  r[0] = (__bf16)lo;
+  r[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, r);
 }
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(pack_bf16x2(f, 0.f) & 0xffffu); }
 
 // 8 fp32 -> one MFMA operand of 8 bf16.
 __device__ __forceinline__ bf16x8 to_bf16x8(const float* v) {
@@ -115,11 +121,17 @@ struct SeqInfo {
 
 enum : int32_t { kItemPrefill = 0, kItemDecode = 1 };
 
+// One workgroup's work, with its sequence's facts folded in so the kernel's
+// prologue needs one dependent load less.
 struct WorkItem {
-  int32_t kind;   // kItemPrefill / kItemDecode
+  int32_t kind_b;        // kind | (b << 8); b = prefill: wave-group id, decode: kv-head group
   int32_t seq;
-  int32_t a;      // prefill: kv head;       decode: split index
-  int32_t b;      // prefill: wave-group id; decode: kv-head group (4 heads)
+  int32_t a;             // prefill: kv head; decode: split index
+  int32_t q_row_start;
+  int32_t ctx_len;
+  int32_t q_len;
+  int32_t nsplits;
+  int32_t partial_base;
 };
 
 }  // namespace gllm

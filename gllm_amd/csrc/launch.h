@@ -65,10 +65,13 @@ struct AttnArgs {
   const WorkItem* items;
   int32_t n_items;
   int32_t num_seqs;
+  int64_t n_partials;
   float* partials;            // [n_partials][16][D] fp32
   float* partial_ml;          // [n_partials][16][2] fp32 (running max in log2 units, sum)
   int32_t* counters;          // [num_seqs * Hkv] split tickets, zero between launches
   int32_t split_len;
+  int32_t heads_per_wg;       // decode: kv heads per workgroup (1, 2, 4, 8)
+  int32_t decode_waves;       // decode: waves per workgroup (8)
   int32_t num_q_heads, num_kv_heads, head_dim;
   float scale;
   int32_t dtype, kv_dtype;

@@ -120,7 +120,7 @@ class AttentionPlan:
 
     def __init__(self, query_lens, seq_lens, *, num_q_heads: int, num_kv_heads: int, head_dim: int,
                  block_size: int, dtype: torch.dtype, device, q_seq_stride: int = 0,
-                 split_tokens: int = 0):
+                 split_tokens: int = 0, heads_per_wg: int = 0):
         ql = [int(x) for x in query_lens]
         sl = [int(x) for x in seq_lens]
         if len(ql) != len(sl):
@@ -132,7 +132,7 @@ class AttentionPlan:
         sa = (ctypes.c_int32 * max(len(sl), 1))(*sl)
         _lib.check(lib.gllm_attn_plan_create(ctypes.byref(self._h), qa, sa, len(ql), q_seq_stride,
                                              num_q_heads, num_kv_heads, head_dim, block_size,
-                                             _lib.dtype_code(dtype), split_tokens))
+                                             _lib.dtype_code(dtype), split_tokens, heads_per_wg))
         self.num_q_heads, self.num_kv_heads, self.head_dim = num_q_heads, num_kv_heads, head_dim
         self.block_size, self.dtype = block_size, dtype
         self.query_lens, self.seq_lens = ql, sl
@@ -145,9 +145,10 @@ class AttentionPlan:
 
     @property
     def info(self) -> dict:
-        arr = (ctypes.c_int64 * 6)()
-        _lib.check(self._lib.gllm_attn_plan_info(self._h, arr, 6))
-        keys = ("work_items", "split_tokens", "decode_seqs", "prefill_seqs", "partials", "rows")
+        arr = (ctypes.c_int64 * 8)()
+        _lib.check(self._lib.gllm_attn_plan_info(self._h, arr, 8))
+        keys = ("work_items", "split_tokens", "decode_seqs", "prefill_seqs", "partials", "rows", "heads_per_wg",
+                "decode_waves")
         return dict(zip(keys, list(arr)))
 
     def __del__(self):

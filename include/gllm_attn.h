@@ -86,20 +86,23 @@ int gllm_rope_kv_write(const void* q, void* q_out, const void* k, const void* v,
  * (q_seq_stride = the padded T_q of the reference's [B, T_q, ...] layout), or,
  * if q_seq_stride == 0, packed rows (cumulative query_lens).  seq_lens[i] =
  * context + query length, as llm.py:233-236.  split_tokens = context tokens
- * per decode split (multiple of 32; 0 = choose from the batch and the CU
- * count).  No device work happens here.
+ * per decode split (multiple of 32) and decode_heads_per_wg = kv heads one
+ * decode workgroup serves (1, 2, 4 or 8); 0 lets the planner choose both from
+ * the batch and the CU count.  No device work happens here.
  */
 int gllm_attn_plan_create(gllm_attn_plan** plan, const int32_t* query_lens,
                           const int32_t* seq_lens, int32_t num_seqs, int64_t q_seq_stride,
                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-                          int32_t block_size, int32_t dtype, int32_t split_tokens);
+                          int32_t block_size, int32_t dtype, int32_t split_tokens,
+                          int32_t decode_heads_per_wg);
 /* Device bytes the plan needs (work list, split partials, tickets). */
 size_t gllm_attn_plan_workspace_bytes(const gllm_attn_plan* plan);
 /* Stream-ordered upload of the plan into `workspace` (>= workspace_bytes).
  * The workspace must stay alive and untouched while launches use the plan. */
 int gllm_attn_plan_upload(gllm_attn_plan* plan, void* workspace, size_t workspace_bytes, void* stream);
 /* Plan facts: [0] work items, [1] split length, [2] decode-path sequences,
- * [3] prefill-path sequences, [4] split partials, [5] total query rows. */
+ * [3] prefill-path sequences, [4] split partials, [5] total query rows,
+ * [6] kv heads per decode workgroup, [7] waves per decode workgroup. */
 int gllm_attn_plan_info(const gllm_attn_plan* plan, int64_t* info, int32_t n);
 int gllm_attn_plan_destroy(gllm_attn_plan* plan);
 

@@ -33,13 +33,14 @@ def test_planner_host_logic():
     h = ctypes.c_void_p()
     ql = (ctypes.c_int32 * 3)(1, 1, 40)
     sl = (ctypes.c_int32 * 3)(100, 2000, 80)
-    assert lib.gllm_attn_plan_create(ctypes.byref(h), ql, sl, 3, 0, 32, 8, 64, 16, _lib.DTYPE_BF16, 128) == 0
-    info = (ctypes.c_int64 * 6)()
-    assert lib.gllm_attn_plan_info(h, info, 6) == 0
-    items, split, ndec, npf, parts, rows = list(info)
-    # seq0: 1 split x 2 groups of 4 kv heads; seq1: 16 splits x 2; seq2 (40 rows x G=4 > 16):
-    # prefill, ceil(4 * 2 row tiles / 4) = 2 workgroups x 8 kv heads
-    assert (items, split, ndec, npf, parts, rows) == (2 + 32 + 16, 128, 2, 1, 8 * 16, 42)
+    assert lib.gllm_attn_plan_create(ctypes.byref(h), ql, sl, 3, 0, 32, 8, 64, 16, _lib.DTYPE_BF16, 128, 8) == 0
+    info = (ctypes.c_int64 * 7)()
+    assert lib.gllm_attn_plan_info(h, info, 7) == 0
+    items, split, ndec, npf, parts, rows, hw = list(info)
+    assert hw == 8
+    # seq0: 1 split; seq1: 16 splits (one workgroup serves all 8 kv heads);
+    # seq2 (40 rows x G=4 > 16): prefill, ceil(4 * 2 row tiles / 8) = 1 workgroup x 8 kv heads
+    assert (items, split, ndec, npf, parts, rows) == (1 + 16 + 8, 128, 2, 1, 8 * 16, 42)
     assert lib.gllm_attn_plan_workspace_bytes(h) > 8 * 16 * 64 * 4
     assert lib.gllm_attn_plan_destroy(h) == 0
 
@@ -51,6 +52,7 @@ def test_planner_host_logic():
     (dict(bs=12), _lib.EUNSUPPORTED),              # block size not a power of two
     (dict(d=96), _lib.EUNSUPPORTED),               # bf16 head_dim
     (dict(split=48), _lib.EINVAL),                 # split not a multiple of 32
+    (dict(hw=3), _lib.EINVAL),                     # heads per decode workgroup
 ])
 def test_planner_rejects(args, code):
     lib = _lib.load()
@@ -59,7 +61,7 @@ def test_planner_rejects(args, code):
     h = ctypes.c_void_p()
     rc = lib.gllm_attn_plan_create(ctypes.byref(h), (ctypes.c_int32 * 1)(*ql), (ctypes.c_int32 * 1)(*sl), 1, 0,
                                    args.get("hq", 8), args.get("hkv", 2), args.get("d", 64), args.get("bs", 16),
-                                   _lib.DTYPE_BF16, args.get("split", 0))
+                                   _lib.DTYPE_BF16, args.get("split", 0), args.get("hw", 0))
     assert rc == code
     assert lib.gllm_attn_last_error()
     assert not h.value
