@@ -320,28 +320,38 @@ __global__ void __launch_bounds__(64) merge_splits_kernel(AttnArgs a) {
 // ============================================================== prefill
 template <int D> struct PrefillCfg {
   static constexpr int kBN = 64;                   // keys per tile
-  static constexpr int kKRow = D * 2 + 16;         // K row stride in LDS (bytes)
-  static constexpr int kVRow = D * 2 + 32;         // V row stride in LDS (bytes)
-  static constexpr int kLdsBytes = kBN * (kKRow + kVRow);
+  static constexpr int kRow = D * 2;               // bytes per K/V row in LDS (16-byte chunks XOR-swizzled)
+  static constexpr int kTile = kBN * kRow;         // bytes per K (or V) tile
+  static constexpr int kBidCache = 1024;           // block ids cached per workgroup
+  static constexpr int kLdsBytes = 4 * kTile + kBidCache * 4;   // K, V double-buffered + block ids
 };
+
+// Logical 16-byte chunk c of LDS row r lives at chunk c ^ (r mod chunks-per-row):
+// the 16 rows one MFMA operand read touches land in 16 different bank groups.
+template <int D>
+__device__ __forceinline__ int swz(int r, int c) { return c ^ (r & (D / 8 - 1)); }
 
 // One 8-wave workgroup: each wave owns 32 query rows of one query head; the
 // waves cover (head, row block) pairs of one kv head, so every K/V tile staged
-// in LDS serves up to 8 x 32 query rows.
+// in LDS serves up to 8 x 32 query rows.  K/V tiles of 64 keys are double
+// buffered in LDS (one barrier per tile); the global loads for tile t+2 are
+// in flight while tile t is computed.  Softmax: exp argument as one FMA,
+// lazy rescale of the running max (exact).
 // Paged mode: keys come from the cache through the block table, causal mask.
 // Dense mode (DENSE): keys from k/v [B, T, Hkv, D], additive bias [B, T_q, T].
 template <int D, bool DENSE>
 __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it, int seq, int kvh, int wgrp, char* lds) {
-  constexpr int NQ = D / 16;   // Q operand chunks (16 dims)
-  constexpr int NO = D / 32;   // output blocks (32 dims)
-  constexpr int BN = PrefillCfg<D>::kBN;
-  constexpr int KR = PrefillCfg<D>::kKRow;
-  constexpr int VR = PrefillCfg<D>::kVRow;
+  using Cfg = PrefillCfg<D>;
+  constexpr int NQ = D / 16;               // Q operand chunks (16 dims)
+  constexpr int NO = D / 32;               // output blocks (32 dims)
+  constexpr int BN = Cfg::kBN;
+  constexpr int RW = Cfg::kRow;
   constexpr int CPR = D / 8;               // 16-byte chunks per key row
   constexpr int NT = 64 * kWaves;          // threads per workgroup
   constexpr int CH = BN * CPR / NT;        // chunks per thread per tile
-  char* ldsK = lds;
-  char* ldsV = lds + BN * KR;
+  static_assert(CH >= 1 && BN * CPR % NT == 0, "tile / workgroup mismatch");
+  char* const ldsKV = lds;                 // K[buf] at buf * kTile, V[buf] at (2 + buf) * kTile
+  int32_t* const lbid = reinterpret_cast<int32_t*>(lds + 4 * Cfg::kTile);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n = lane & 31, h = lane >> 5;
 
@@ -375,6 +385,17 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   const int64_t qrow = qstart + rr;
   const int qh = kvh * G + g;
 
+  // block ids of keys [0, kend_wg) -> LDS (first kBidCache blocks; any beyond
+  // are read from the table directly)
+  const int32_t* bt = DENSE ? nullptr : a.block_table + (int64_t)seq * a.block_table_stride;
+  if (!DENSE) {
+    const int nblk = ((kend_wg - 1) >> a.block_shift) + 1;
+    for (int i = tid; i < min(nblk, Cfg::kBidCache); i += NT) {
+      const uint32_t b = (uint32_t)bt[i];
+      lbid[i] = b < (uint64_t)a.num_blocks ? (int32_t)b : 0;  // never address outside the pool
+    }
+  }
+
   // Q as the B operand of S^T = K Q^T: lane holds Q[row n][16kk + 8h + i].
   bf16x8 qB[NQ];
   {
@@ -397,26 +418,47 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 #pragma unroll
     for (int kk = 0; kk < NQ; ++kk) qB[kk] = to_bf16x8(x[kk]);
   }
+  if (!DENSE) __syncthreads();  // block ids visible
 
-  const int32_t* bt = DENSE ? nullptr : a.block_table + (int64_t)seq * a.block_table_stride;
-  u32x4 kreg[CH], vreg[CH];
+  const uint32_t sbytes = (uint32_t)(a.cache_slot_stride * 2);
+  const uint32_t bmask = a.block_size - 1;
+  u32x4 kst[CH], vst[CH];
   auto gload = [&](int ts) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + NT * i;
-      const int key = c / CPR, part = c - key * CPR;
+      const int key = c / CPR, ch = c - key * CPR;
       const int p = min(ts + key, kend_wg - 1);
-      const __bf16 *kp, *vp;
+      const char *kp, *vp;
       if (DENSE) {
-        kp = (const __bf16*)a.k + (int64_t)seq * a.k_batch_stride + (int64_t)p * a.k_row_stride;
-        vp = (const __bf16*)a.v + (int64_t)seq * a.v_batch_stride + (int64_t)p * a.v_row_stride;
+        kp = (const char*)a.k + ((int64_t)seq * a.k_batch_stride + (int64_t)p * a.k_row_stride + (int64_t)kvh * D) * 2;
+        vp = (const char*)a.v + ((int64_t)seq * a.v_batch_stride + (int64_t)p * a.v_row_stride + (int64_t)kvh * D) * 2;
       } else {
-        const int64_t slot = paged_slot(a, bt, p);
-        kp = (const __bf16*)a.k_cache + slot * a.cache_slot_stride;
-        vp = (const __bf16*)a.v_cache + slot * a.cache_slot_stride;
+        const int bi = p >> a.block_shift;
+        uint32_t blk;
+        if (bi < Cfg::kBidCache) {
+          blk = (uint32_t)lbid[bi];
+        } else {
+          blk = (uint32_t)bt[bi];
+          if (blk >= (uint64_t)a.num_blocks) blk = 0;
+        }
+        const uint64_t off = (uint64_t)(blk * (uint32_t)a.block_size + ((uint32_t)p & bmask)) * sbytes +
+                             (uint64_t)kvh * D * 2;
+        kp = (const char*)a.k_cache + off;
+        vp = (const char*)a.v_cache + off;
       }
-      kreg[i] = ld16(kp + (int64_t)kvh * D + 8 * part);
-      vreg[i] = ld16(vp + (int64_t)kvh * D + 8 * part);
+      kst[i] = ld16(kp + ch * 16);
+      vst[i] = ld16(vp + ch * 16);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + NT * i;
+      const int key = c / CPR, ch = c - key * CPR;
+      const int o = key * RW + (swz<D>(key, ch) << 4);
+      *reinterpret_cast<u32x4*>(ldsKV + buf * Cfg::kTile + o) = kst[i];
+      *reinterpret_cast<u32x4*>(ldsKV + (2 + buf) * Cfg::kTile + o) = vst[i];
     }
   };
 
@@ -428,97 +470,100 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 #pragma unroll
     for (int j = 0; j < 16; ++j) o[db][j] = 0.f;
 
-  const int ntiles = (kend_wg + BN - 1) / BN;
-  gload(0);
-  for (int t = 0; t < ntiles; ++t) {
-    const int ts = t * BN;
+  auto compute = [&](const char* ldsK, const char* ldsV, int ts) {
+    f32x16 s[2];
 #pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int c = tid + NT * i;
-      const int key = c / CPR, part = c - key * CPR;
-      *reinterpret_cast<u32x4*>(ldsK + key * KR + part * 16) = kreg[i];
-      *reinterpret_cast<u32x4*>(ldsV + key * VR + part * 16) = vreg[i];
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) s[kb][j] = 0.f;
+      const int row = 32 * kb + n;
+#pragma unroll
+      for (int kk = 0; kk < NQ; ++kk) {
+        const u32x4 ka = *reinterpret_cast<const u32x4*>(ldsK + row * RW + (swz<D>(row, 2 * kk + h) << 4));
+        s[kb] = mfma32(as_bf16x8(ka), qB[kk], s[kb]);
+      }
     }
-    __syncthreads();
-    if (t + 1 < ntiles) gload(ts + BN);
-    if (wact && ts < kend_w) {
-      f32x16 s[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) s[kb][j] = 0.f;
-#pragma unroll
-        for (int kk = 0; kk < NQ; ++kk) {
-          const u32x4 ka = *reinterpret_cast<const u32x4*>(ldsK + (32 * kb + n) * KR + (16 * kk + 8 * h) * 2);
-          s[kb] = mfma32(as_bf16x8(ka), qB[kk], s[kb]);
-        }
-      }
-      // lane holds S[key ts + 32kb + 8(j/4) + 4h + j%4][row n]
-      float sv[2][16];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) sv[kb][j] = s[kb][j] * sl2;
-      if (DENSE) {
-        const __bf16* bp = (const __bf16*)a.bias + (int64_t)seq * a.bias_batch_stride + (int64_t)rr * a.bias_row_stride;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int jq = 0; jq < 4; ++jq) {
-            const int key0 = ts + 32 * kb + 8 * jq + 4 * h;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int key = key0 + e;
-              const float bv = key < T ? (float)bp[key] : kNegInf;
-              sv[kb][4 * jq + e] = __builtin_fmaf(bv, kLog2e, sv[kb][4 * jq + e]);
-            }
-          }
-      } else if (ts + BN - 1 > ctx + r0) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int key = ts + 32 * kb + 8 * (j >> 2) + 4 * h + (j & 3);
-            if (key > vis) sv[kb][j] = kNegInf;
-          }
-      }
-      float tmax = sv[0][0];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) tmax = fmaxf(tmax, sv[kb][j]);
-      tmax = max_xor32(tmax);
-      const float mn = fmaxf(m, tmax);
-      const float mu = mn == kNegInf ? 0.f : mn;
-      const float alpha = fast_exp2(m - mu);
-      float ps = 0.f;
+    // lane holds raw scores S[key ts + 32kb + 8(j/4) + 4h + j%4][row n]
+    if (DENSE) {
+      const __bf16* bp = (const __bf16*)a.bias + (int64_t)seq * a.bias_batch_stride + (int64_t)rr * a.bias_row_stride;
+      const float inv_scale = 1.f / a.scale;   // bias is added in natural-log units
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          sv[kb][j] = fast_exp2(sv[kb][j] - mu);
-          ps += sv[kb][j];
+          const int key = ts + 32 * kb + 8 * (j >> 2) + 4 * h + (j & 3);
+          const float bv = key < T ? (float)bp[key] : kNegInf;
+          s[kb][j] = __builtin_fmaf(bv, inv_scale, s[kb][j]);
         }
-      lsum = lsum * alpha + ps;
-      m = mn;
-#pragma unroll
-      for (int db = 0; db < NO; ++db) o[db] *= alpha;
-      const int g4 = lane >> 4, i16 = lane & 15;
+    } else if (ts + BN - 1 > ctx + r0) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int tp = 0; tp < 2; ++tp) {
-          const bf16x8 pb = to_bf16x8(&sv[kb][8 * tp]);
-          const int row1 = 32 * kb + 16 * tp + 4 * h + (i16 >> 2);
-#pragma unroll
-          for (int db = 0; db < NO; ++db) {
-            const int col = 32 * db + 16 * (g4 & 1) + 4 * (i16 & 3);
-            const u32x2 r1 = lds_read_tr16(ldsV + row1 * VR + col * 2);
-            const u32x2 r2 = lds_read_tr16(ldsV + (row1 + 8) * VR + col * 2);
-            const u32x4 av = {r1[0], r1[1], r2[0], r2[1]};
-            o[db] = mfma32(as_bf16x8(av), pb, o[db]);
-          }
+        for (int j = 0; j < 16; ++j) {
+          const int key = ts + 32 * kb + 8 * (j >> 2) + 4 * h + (j & 3);
+          if (key > vis) s[kb][j] = kNegInf;
         }
+    }
+    float tmax = kNegInf;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 16; j += 2) tmax = __builtin_fmaxf(tmax, __builtin_fmaxf(s[kb][j], s[kb][j + 1]));
+    tmax = max_xor32(tmax) * sl2;
+    // Lazy rescale: the running max only moves when a row's tile max exceeds
+    // it by more than 8 (log2 units), so p <= 2^8; numerator and denominator
+    // share m, so the result is exact.
+    if (__builtin_amdgcn_ballot_w64(tmax > m + 8.f)) {
+      const float mn = tmax > m + 8.f ? tmax : m;
+      const float alpha = fast_exp2(m - (mn == kNegInf ? 0.f : mn));
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < NO; ++db) o[db] *= alpha;
+      m = mn;
+    }
+    const float nmu = m == kNegInf ? 0.f : -m;
+    float ps = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        s[kb][j] = fast_exp2(__builtin_fmaf(s[kb][j], sl2, nmu));
+        ps += s[kb][j];
+      }
+    lsum += ps;
+    const int g4 = lane >> 4, i16 = lane & 15;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int tp = 0; tp < 2; ++tp) {
+        float pv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] = s[kb][8 * tp + e];
+        const bf16x8 pb = to_bf16x8(pv);
+        const int row1 = 32 * kb + 16 * tp + 4 * h + (i16 >> 2);
+#pragma unroll
+        for (int db = 0; db < NO; ++db) {
+          const int cb = 64 * db + 32 * (g4 & 1) + 8 * (i16 & 3);  // byte column
+          const int c = cb >> 4, within = cb & 15;
+          const u32x2 r1 = lds_read_tr16(ldsV + row1 * RW + (swz<D>(row1, c) << 4) + within);
+          const u32x2 r2 = lds_read_tr16(ldsV + (row1 + 8) * RW + (swz<D>(row1 + 8, c) << 4) + within);
+          const u32x4 av = {r1[0], r1[1], r2[0], r2[1]};
+          o[db] = mfma32(as_bf16x8(av), pb, o[db]);
+        }
+      }
+  };
+
+  const int ntiles = (kend_wg + BN - 1) / BN;
+  gload(0);
+  lstore(0);
+  if (ntiles > 1) gload(BN);
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int cur = t & 1, ts = t * BN;
+    if (wact && ts < kend_w) compute(ldsKV + cur * Cfg::kTile, ldsKV + (2 + cur) * Cfg::kTile, ts);
+    if (t + 1 < ntiles) {
+      lstore(cur ^ 1);                     // tile t+1, loaded during the previous iteration
+      if (t + 2 < ntiles) gload(ts + 2 * BN);
     }
     __syncthreads();
   }
