@@ -173,6 +173,8 @@ def main():
     ap.add_argument("--hw", type=int, default=0, help="kv heads per decode workgroup (0 = planner's choice)")
     ap.add_argument("--copies", type=int, default=4, help="KV pool copies rotated for config (b)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also run a plain 256 MiB device copy (known bytes) for counter calibration")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: --gpus must be 1 "
@@ -198,6 +200,12 @@ def main():
         r, _, _ = bench_decode(workloads.config_e(), 1, args.warmup, max(5, args.steps // 3), args.split, dev, args.hw)
         extra["long_decode_70b"] = r
         torch.cuda.empty_cache()
+    if args.calibrate:
+        src = torch.empty(128 << 20, dtype=torch.bfloat16, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     cpu = None
     if head is not None and not args.no_cpu:
         cpu = cpu_baseline_decode(x0, head["bytes_per_launch"])

@@ -363,6 +363,8 @@ int gllm_paged_attention(const gllm_attn_plan* p, const void* q, int64_t q_row_s
   if (q_row_stride < hd || out_row_stride < hd) return fail(GLLM_ATTN_EINVAL, "q/out row stride < num_q_heads * head_dim");
   if (cache_slot_stride < (int64_t)p->Hkv * p->D) return fail(GLLM_ATTN_EINVAL, "cache_slot_stride too small");
   if (num_blocks <= 0) return fail(GLLM_ATTN_EINVAL, "num_blocks must be > 0");
+  if ((uint64_t)num_blocks * (uint64_t)p->bs >= (1ull << 32))
+    return fail(GLLM_ATTN_EUNSUPPORTED, "pool of %lld blocks x %d slots exceeds 2^32 slots", (long long)num_blocks, p->bs);
   if (block_table_stride <= 0) return fail(GLLM_ATTN_EINVAL, "block_table_stride must be > 0");
   if (rope_mode != GLLM_ROPE_NONE && rope_mode != GLLM_ROPE_BY_POSITION && rope_mode != GLLM_ROPE_BY_ROW)
     return fail(GLLM_ATTN_EINVAL, "rope_mode %d", rope_mode);
