@@ -53,7 +53,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 struct gllm_attn_plan {
   int32_t num_seqs = 0, Hq = 0, Hkv = 0, D = 0, bs = 0, dtype = 0;
   int32_t split_len = 0, max_q = 0;
-  int32_t n_decode_seqs = 0, n_prefill_seqs = 0, heads_per_wg = 8, decode_waves = 8;
+  int32_t n_decode_seqs = 0, n_prefill_seqs = 0, heads_per_wg = 8, decode_waves = 8, prefill_waves = 8;
   int64_t total_rows = 0;
   int64_t n_partials = 0;
   std::vector<SeqInfo> seqs;
@@ -218,6 +218,9 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
     best_S = std::min(best_S, cap);
     p->heads_per_wg = best_hw;
     p->decode_waves = best_nw;
+    // Prefill: 8-wave workgroups, one per CU (4-stage K/V ring in LDS).
+    const int pw = 8;
+    p->prefill_waves = pw;
     const int hgroups = (num_kv_heads + best_hw - 1) / best_hw;
     const int64_t S = best_S;
     p->split_len = (int32_t)S;
@@ -240,10 +243,10 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
       } else {
         ++p->n_prefill_seqs;
         const int nrb = (s.q_len + 31) / 32;
-        const int nwg = (G * nrb + 7) / 8;
+        const int nwg = (G * nrb + pw - 1) / pw;
         for (int h = 0; h < num_kv_heads; ++h)
           for (int w = 0; w < nwg; ++w) {
-            const int last_combo = std::min(w * 8 + 7, G * nrb - 1);
+            const int last_combo = std::min(w * pw + pw - 1, G * nrb - 1);
             const int64_t kend = s.ctx_len + std::min(s.q_len - 1, (last_combo / G) * 32 + 31) + 1;
             pf.push_back({kend, WorkItem{kItemPrefill | (w << 8), i, h, s.q_row_start, s.ctx_len, s.q_len, 0, 0}});
           }
@@ -252,15 +255,34 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
     // Longest work first so the tail is made of short items.
     std::stable_sort(pf.begin(), pf.end(), [](const Keyed& x, const Keyed& y) { return x.work > y.work; });
     std::stable_sort(dc.begin(), dc.end(), [](const Keyed& x, const Keyed& y) { return x.work > y.work; });
-    // Snake order: workgroups are dispatched slot-major (item k and item
-    // k + cus land on the same CU while every slot is free), so alternate the
-    // direction every `cus` items; each CU then pairs long work with short.
+    // Workgroups are dispatched slot-major: while every slot is free, item k
+    // and item k + cus land on the same CU, and the older (first) one wins
+    // the CU's memory pipeline.
     std::vector<Keyed> all;
     all.reserve(pf.size() + dc.size());
-    for (auto& k : pf) all.push_back(k);
-    for (auto& k : dc) all.push_back(k);
-    for (size_t c0 = cus, chunk = 1; c0 < all.size(); c0 += cus, ++chunk)
-      if (chunk & 1) std::reverse(all.begin() + c0, all.begin() + std::min(all.size(), c0 + (size_t)cus));
+    const size_t ncu = (size_t)cus;
+    if (pf.empty() && head_dim == 64 && dc.size() > ncu && dc.size() <= 2 * ncu) {
+      // Decode items that all fit at once, two per CU: CU k pairs the k-th
+      // longest with the k-th shortest item (equal work per CU) and gets the
+      // short one first, so it finishes quickly and the long one then has the
+      // CU's full bandwidth (long-first starves the short item until the long
+      // one is done, then leaves it alone on the CU).  CUs without a pair take
+      // the middle items.
+      const size_t n = dc.size(), m = n - ncu;   // m paired CUs
+      all.resize(n);
+      for (size_t k = 0; k < m; ++k) {
+        all[k] = dc[n - 1 - k];                  // first slot: short
+        all[ncu + k] = dc[k];                    // second slot: long
+      }
+      for (size_t k = m; k < ncu; ++k) all[k] = dc[k];   // middle items, alone on their CU
+    } else {
+      // Snake order: alternate the direction every `cus` items, so each CU
+      // pairs long work with short.
+      for (auto& k : pf) all.push_back(k);
+      for (auto& k : dc) all.push_back(k);
+      for (size_t c0 = ncu, chunk = 1; c0 < all.size(); c0 += ncu, ++chunk)
+        if (chunk & 1) std::reverse(all.begin() + c0, all.begin() + std::min(all.size(), c0 + ncu));
+    }
     p->items.reserve(all.size());
     for (auto& k : all) p->items.push_back(k.it);
     if (p->items.size() > (size_t)INT32_MAX) {
@@ -300,9 +322,9 @@ size_t gllm_attn_plan_workspace_bytes(const gllm_attn_plan* p) { return p ? p->w
 
 int gllm_attn_plan_info(const gllm_attn_plan* p, int64_t* info, int32_t n) {
   if (!p || !info) return fail(GLLM_ATTN_EINVAL, "null plan or info");
-  const int64_t v[8] = {(int64_t)p->items.size(), p->split_len, p->n_decode_seqs, p->n_prefill_seqs,
-                        p->n_partials, p->total_rows, p->heads_per_wg, p->decode_waves};
-  for (int i = 0; i < n && i < 8; ++i) info[i] = v[i];
+  const int64_t v[9] = {(int64_t)p->items.size(), p->split_len, p->n_decode_seqs, p->n_prefill_seqs,
+                        p->n_partials, p->total_rows, p->heads_per_wg, p->decode_waves, p->prefill_waves};
+  for (int i = 0; i < n && i < 9; ++i) info[i] = v[i];
   return ok();
 }
 
@@ -329,14 +351,14 @@ int gllm_attn_plan_upload(gllm_attn_plan* p, void* workspace, size_t bytes, void
 int gllm_attn_plan_destroy(gllm_attn_plan* p) {
   if (!p) return ok();
   if (p->upload_done) {
-    hipEventSynchronize(p->upload_done);  // the staging copy must finish before the free
-    hipEventDestroy(p->upload_done);
+    (void)hipEventSynchronize(p->upload_done);  // the staging copy must finish before the free
+    (void)hipEventDestroy(p->upload_done);
   }
   if (p->pinned) {
     if (p->pinned_is_host_malloc)
       std::free(p->pinned);
     else
-      hipHostFree(p->pinned);
+      (void)hipHostFree(p->pinned);
   }
   delete p;
   return ok();
@@ -392,6 +414,7 @@ int gllm_paged_attention(const gllm_attn_plan* p, const void* q, int64_t q_row_s
   a.n_partials = p->n_partials;
   a.heads_per_wg = p->heads_per_wg;
   a.decode_waves = p->decode_waves;
+  a.prefill_waves = p->prefill_waves;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == GLLM_DTYPE_BF16)
     return hip_check(launch_paged_attention_bf16(a, p->n_prefill_seqs > 0, p->n_decode_seqs > 0, st),

@@ -72,6 +72,7 @@ struct AttnArgs {
   int32_t split_len;
   int32_t heads_per_wg;       // decode: kv heads per workgroup (1, 2, 4, 8)
   int32_t decode_waves;       // decode: waves per workgroup (8)
+  int32_t prefill_waves;      // prefill: waves per workgroup (8)
   int32_t num_q_heads, num_kv_heads, head_dim;
   float scale;
   int32_t dtype, kv_dtype;

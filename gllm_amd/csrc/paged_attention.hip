@@ -318,40 +318,66 @@ __global__ void __launch_bounds__(64) merge_splits_kernel(AttnArgs a) {
 }
 
 // ============================================================== prefill
-template <int D> struct PrefillCfg {
+template <int D, int NS> struct PrefillCfg {
   static constexpr int kBN = 64;                   // keys per tile
   static constexpr int kRow = D * 2;               // bytes per K/V row in LDS (16-byte chunks XOR-swizzled)
   static constexpr int kTile = kBN * kRow;         // bytes per K (or V) tile
+  static constexpr int kStage = 2 * kTile;         // one pipeline stage: K tile, then V tile
+  static constexpr int kStages = NS;               // LDS ring: tiles t+1 .. t+NS-1 in flight while t is computed
   static constexpr int kBidCache = 1024;           // block ids cached per workgroup
-  static constexpr int kLdsBytes = 4 * kTile + kBidCache * 4;   // K, V double-buffered + block ids
+  static constexpr int kLdsBytes = kStages * kStage + kBidCache * 4;
 };
 
-// Logical 16-byte chunk c of LDS row r lives at chunk c ^ (r mod chunks-per-row):
-// the 16 rows one MFMA operand read touches land in 16 different bank groups.
-template <int D>
-__device__ __forceinline__ int swz(int r, int c) { return c ^ (r & (D / 8 - 1)); }
+// Direct global -> LDS copy of 16 bytes per lane: lane l's bytes land at
+// lds_base + 16 l (lds_base wave-uniform, in M0).  Written as inline asm so
+// the compiler does not wait for every outstanding copy before each LDS read;
+// the kernel waits for its own copies with wait_vmcnt before the barrier that
+// publishes a stage.
+__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_base) : "memory", "m0");
+}
+// s_waitcnt vmcnt(N) leaving the other counters alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
 
-// One 8-wave workgroup: each wave owns 32 query rows of one query head; the
+// Logical 16-byte chunk c of LDS row r is stored at chunk c ^ pf_swz(r).  The
+// pattern keeps the three access shapes of a tile free of bank conflicts:
+//   QK operand reads (ds_read_b128): 16 lanes read one logical chunk of 16
+//     consecutive rows -> pf_swz is a bijection on r mod 16 (D = 128), or on
+//     each parity class of r mod 16 (D = 64, two rows per 256-byte bank line);
+//   PV operand reads (ds_read_b64_tr_b16): 32 lanes read chunks 4j..4j+3 of
+//     rows 4i..4i+3 -> the upper bits of pf_swz differ across those rows;
+//   tile stores: the lanes storing one row write all its chunks.
+template <int D>
+__device__ __forceinline__ int pf_swz(int r) {
+  return D == 128 ? (((r & 3) << 2) | ((r >> 2) & 3)) : ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
+}
+
+// One NW-wave workgroup: each wave owns 32 query rows of one query head; the
 // waves cover (head, row block) pairs of one kv head, so every K/V tile staged
-// in LDS serves up to 8 x 32 query rows.  K/V tiles of 64 keys are double
-// buffered in LDS (one barrier per tile); the global loads for tile t+2 are
-// in flight while tile t is computed.  Softmax: exp argument as one FMA,
-// lazy rescale of the running max (exact).
-// Paged mode: keys come from the cache through the block table, causal mask.
-// Dense mode (DENSE): keys from k/v [B, T, Hkv, D], additive bias [B, T_q, T].
-template <int D, bool DENSE>
+// in LDS serves up to NW x 32 query rows.  K/V tiles of 64 keys stream from
+// HBM straight into an NS-stage LDS ring (global_load_lds, NS/2 tiles ahead,
+// one barrier per NS/2 tiles).  A tile is processed as two 32-key halves: S^T = K
+// Q^T for both halves is issued first, so the softmax of half 0 runs on the
+// VALU while the MFMAs of half 1 execute, and the softmax of half 1 overlaps
+// O^T += V^T P^T of half 0.  Softmax: exp argument as one FMA, lazy rescale
+// of the running max (exact), branch-free except the rare rescale of O.
+// Paged mode: keys through the block table, causal mask on diagonal tiles
+// only.  Dense mode (DENSE): keys from k/v [B, T, Hkv, D], additive bias
+// [B, T_q, T] on every tile.
+template <int D, bool DENSE, int NW, int NS>
 __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it, int seq, int kvh, int wgrp, char* lds) {
-  using Cfg = PrefillCfg<D>;
+  using Cfg = PrefillCfg<D, NS>;
   constexpr int NQ = D / 16;               // Q operand chunks (16 dims)
   constexpr int NO = D / 32;               // output blocks (32 dims)
   constexpr int BN = Cfg::kBN;
   constexpr int RW = Cfg::kRow;
   constexpr int CPR = D / 8;               // 16-byte chunks per key row
-  constexpr int NT = 64 * kWaves;          // threads per workgroup
-  constexpr int CH = BN * CPR / NT;        // chunks per thread per tile
-  static_assert(CH >= 1 && BN * CPR % NT == 0, "tile / workgroup mismatch");
-  char* const ldsKV = lds;                 // K[buf] at buf * kTile, V[buf] at (2 + buf) * kTile
-  int32_t* const lbid = reinterpret_cast<int32_t*>(lds + 4 * Cfg::kTile);
+  constexpr int NT = 64 * NW;              // threads per workgroup
+  int32_t* const lbid = reinterpret_cast<int32_t*>(lds + Cfg::kStages * Cfg::kStage);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n = lane & 31, h = lane >> 5;
 
@@ -370,12 +396,12 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   }
   const int G = a.num_q_heads / a.num_kv_heads;
   const int nrb = (qlen + 31) / 32;
-  const int combo = wgrp * kWaves + wave;
+  const int combo = wgrp * NW + wave;
   const bool wact = combo < G * nrb;
   const int g = wact ? combo % G : 0;
   const int rblk = wact ? combo / G : 0;
   const int r0 = rblk * 32;
-  const int last_combo = min(wgrp * kWaves + kWaves - 1, G * nrb - 1);
+  const int last_combo = min(wgrp * NW + NW - 1, G * nrb - 1);
   const int kend_wg = DENSE ? T : ctx + min(qlen - 1, (last_combo / G) * 32 + 31) + 1;
   const int kend_w = DENSE ? T : ctx + min(qlen - 1, r0 + 31) + 1;
   const int r = r0 + n;
@@ -396,69 +422,99 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
     }
   }
 
-  // Q as the B operand of S^T = K Q^T: lane holds Q[row n][16kk + 8h + i].
-  bf16x8 qB[NQ];
+  // Q rows (and their cos/sin rows): loads issued now, used after the first
+  // K/V copies are on their way.
+  u32x4 qraw[NQ], craw[NQ / 2], sraw[NQ / 2];
+  const bool q_rope = !DENSE && a.rope_mode != kRopeNone;
   {
     const __bf16* qp = (const __bf16*)a.q + qrow * a.q_row_stride + (int64_t)qh * D + 8 * h;
-    float x[NQ][8];
 #pragma unroll
-    for (int kk = 0; kk < NQ; ++kk) unpack_bf16x8(ld16(qp + 16 * kk), x[kk]);
-    if (!DENSE && a.rope_mode != kRopeNone) {
+    for (int kk = 0; kk < NQ; ++kk) qraw[kk] = ld16(qp + 16 * kk);
+    if (q_rope) {
       const int64_t crow = a.rope_mode == kRopeByPosition ? (int64_t)vis : qrow;
       const __bf16* cp = (const __bf16*)a.rope_cos + crow * a.rope_row_stride + 8 * h;
       const __bf16* sp = (const __bf16*)a.rope_sin + crow * a.rope_row_stride + 8 * h;
 #pragma unroll
       for (int kk = 0; kk < NQ / 2; ++kk) {
-        float c[8], s[8];
-        unpack_bf16x8(ld16(cp + 16 * kk), c);
-        unpack_bf16x8(ld16(sp + 16 * kk), s);
-        rope8_bf16(x[kk], x[kk + NQ / 2], c, s);
+        craw[kk] = ld16(cp + 16 * kk);
+        sraw[kk] = ld16(sp + 16 * kk);
       }
     }
-#pragma unroll
-    for (int kk = 0; kk < NQ; ++kk) qB[kk] = to_bf16x8(x[kk]);
   }
+  bf16x8 qB[NQ];                // filled once the first tile copies are issued
   if (!DENSE) __syncthreads();  // block ids visible
 
+  // Per-lane byte offsets inside a stage (tile-invariant; the stage and the
+  // half / 16-key group go into the instructions' immediate offsets).
+  int koff[NQ];                 // K operand: row n, logical chunk 2kk + h
+#pragma unroll
+  for (int kk = 0; kk < NQ; ++kk) koff[kk] = n * RW + (((2 * kk + h) ^ pf_swz<D>(n)) << 4);
+  int voff[2][NO];              // V^T operand: rows 4h + i16/4 (+8), byte column 64db + 32(g4&1) + 8(i16&3)
+  {
+    const int g4 = lane >> 4, i16 = lane & 15;
+    const int clo = 2 * (g4 & 1) + ((i16 & 3) >> 1);
+#pragma unroll
+    for (int r2 = 0; r2 < 2; ++r2) {
+      const int row = 4 * h + (i16 >> 2) + 8 * r2;
+#pragma unroll
+      for (int db = 0; db < NO; ++db)
+        voff[r2][db] = Cfg::kTile + row * RW + (((4 * db + clo) ^ pf_swz<D>(row)) << 4) + 8 * (i16 & 1);
+    }
+  }
+
+  // K/V tile copy: 1 KB segments (RPS key rows each); wave w copies segments
+  // w, w + NW, ...; lane l fills physical chunk l % CPR of row l / CPR, i.e.
+  // it loads logical chunk (l % CPR) ^ pf_swz(row).
+  constexpr int RPS = 1024 / RW;
+  constexpr int NSEG = BN / RPS;
+  constexpr int CHD = NSEG / NW;          // copies per wave per K (or V) tile
+  static_assert(CHD >= 1 && NSEG % NW == 0, "tile / workgroup mismatch");
   const uint32_t sbytes = (uint32_t)(a.cache_slot_stride * 2);
   const uint32_t bmask = a.block_size - 1;
-  u32x4 kst[CH], vst[CH];
-  auto gload = [&](int ts) {
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+  // Block ids of the DMA rows of the tile starting at key ts (fetched one
+  // tile before the copy is issued, so the copy never waits on LDS).
+  auto dma_bids = [&](int ts, uint32_t (&blk)[CHD]) {
 #pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int c = tid + NT * i;
-      const int key = c / CPR, ch = c - key * CPR;
-      const int p = min(ts + key, kend_wg - 1);
-      const char *kp, *vp;
+    for (int i = 0; i < CHD; ++i) {
       if (DENSE) {
-        kp = (const char*)a.k + ((int64_t)seq * a.k_batch_stride + (int64_t)p * a.k_row_stride + (int64_t)kvh * D) * 2;
-        vp = (const char*)a.v + ((int64_t)seq * a.v_batch_stride + (int64_t)p * a.v_row_stride + (int64_t)kvh * D) * 2;
+        blk[i] = 0;
       } else {
+        const int p = min(ts + (i * NW + wave) * RPS + lane / CPR, kend_wg - 1);
         const int bi = p >> a.block_shift;
-        uint32_t blk;
         if (bi < Cfg::kBidCache) {
-          blk = (uint32_t)lbid[bi];
+          blk[i] = (uint32_t)lbid[bi];
         } else {
-          blk = (uint32_t)bt[bi];
-          if (blk >= (uint64_t)a.num_blocks) blk = 0;
+          blk[i] = (uint32_t)bt[bi];
+          if (blk[i] >= (uint64_t)a.num_blocks) blk[i] = 0;
         }
-        const uint64_t off = (uint64_t)(blk * (uint32_t)a.block_size + ((uint32_t)p & bmask)) * sbytes +
-                             (uint64_t)kvh * D * 2;
-        kp = (const char*)a.k_cache + off;
-        vp = (const char*)a.v_cache + off;
       }
-      kst[i] = ld16(kp + ch * 16);
-      vst[i] = ld16(vp + ch * 16);
     }
   };
-  auto lstore = [&](int buf) {
+  // One copy instruction: chunk row set i of the tile at key ts, K (v = 0)
+  // or V (v = 1), into `stage`.
+  auto dma_one = [&](int ts, int stage, const uint32_t (&blk)[CHD], int i, int v) {
+    const int sg = i * NW + wave;
+    const int row = sg * RPS + lane / CPR;
+    const int lc = (lane % CPR) ^ pf_swz<D>(row);
+    const int p = min(ts + row, kend_wg - 1);
+    const char* src;
+    if (DENSE) {
+      src = v ? (const char*)a.v + ((int64_t)seq * a.v_batch_stride + (int64_t)p * a.v_row_stride + (int64_t)kvh * D) * 2
+              : (const char*)a.k + ((int64_t)seq * a.k_batch_stride + (int64_t)p * a.k_row_stride + (int64_t)kvh * D) * 2;
+    } else {
+      const uint64_t off = (uint64_t)(blk[i] * (uint32_t)a.block_size + ((uint32_t)p & bmask)) * sbytes +
+                           (uint64_t)kvh * D * 2;
+      src = (const char*)(v ? a.v_cache : a.k_cache) + off;
+    }
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(lds0 + stage * Cfg::kStage + v * Cfg::kTile + sg * 1024);
+    lds_dma16(src + lc * 16, dst);
+  };
+  auto dma_issue = [&](int ts, int stage, const uint32_t (&blk)[CHD]) {
 #pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int c = tid + NT * i;
-      const int key = c / CPR, ch = c - key * CPR;
-      const int o = key * RW + (swz<D>(key, ch) << 4);
-      *reinterpret_cast<u32x4*>(ldsKV + buf * Cfg::kTile + o) = kst[i];
-      *reinterpret_cast<u32x4*>(ldsKV + (2 + buf) * Cfg::kTile + o) = vst[i];
+    for (int i = 0; i < CHD; ++i) {
+      dma_one(ts, stage, blk, i, 0);
+      dma_one(ts, stage, blk, i, 1);
     }
   };
 
@@ -470,102 +526,217 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 #pragma unroll
     for (int j = 0; j < 16; ++j) o[db][j] = 0.f;
 
-  auto compute = [&](const char* ldsK, const char* ldsV, int ts) {
-    f32x16 s[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) s[kb][j] = 0.f;
-      const int row = 32 * kb + n;
-#pragma unroll
-      for (int kk = 0; kk < NQ; ++kk) {
-        const u32x4 ka = *reinterpret_cast<const u32x4*>(ldsK + row * RW + (swz<D>(row, 2 * kk + h) << 4));
-        s[kb] = mfma32(as_bf16x8(ka), qB[kk], s[kb]);
-      }
-    }
-    // lane holds raw scores S[key ts + 32kb + 8(j/4) + 4h + j%4][row n]
+  // Softmax of one 32-key half, in pieces that the tile loop interleaves
+  // with MFMAs: lane holds raw scores S[key k0 + 8(j/4) + 4h + j%4][row n].
+  // sm_max: mask, row max, running-max update (lazy rescale: the max only
+  // moves when a row's max exceeds it by more than 8 in log2 units, so
+  // p <= 2^8; numerator and denominator share m, so the result is exact);
+  // sm_exp: p = 2^(s sl2 - m) for 4 scores; sm_sum: row sum; sm_cvt: P as two
+  // bf16 B operands.
+  struct Soft { float alpha, nmu, psum; };
+  auto sm_max = [&](f32x16& s, int k0, bool mask, Soft& q) {
     if (DENSE) {
       const __bf16* bp = (const __bf16*)a.bias + (int64_t)seq * a.bias_batch_stride + (int64_t)rr * a.bias_row_stride;
       const float inv_scale = 1.f / a.scale;   // bias is added in natural-log units
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int j = 0; j < 16; ++j) {
+        const int key = k0 + 8 * (j >> 2) + 4 * h + (j & 3);
+        const float bv = key < T ? (float)bp[key] : kNegInf;
+        s[j] = __builtin_fmaf(bv, inv_scale, s[j]);
+      }
+    } else if (mask) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int key = ts + 32 * kb + 8 * (j >> 2) + 4 * h + (j & 3);
-          const float bv = key < T ? (float)bp[key] : kNegInf;
-          s[kb][j] = __builtin_fmaf(bv, inv_scale, s[kb][j]);
-        }
-    } else if (ts + BN - 1 > ctx + r0) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int key = ts + 32 * kb + 8 * (j >> 2) + 4 * h + (j & 3);
-          if (key > vis) s[kb][j] = kNegInf;
-        }
+      for (int j = 0; j < 16; ++j) {
+        const int key = k0 + 8 * (j >> 2) + 4 * h + (j & 3);
+        s[j] = key > vis ? kNegInf : s[j];
+      }
     }
     float tmax = kNegInf;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int j = 0; j < 16; j += 2) tmax = __builtin_fmaxf(tmax, __builtin_fmaxf(s[kb][j], s[kb][j + 1]));
-    tmax = max_xor32(tmax) * sl2;
-    // Lazy rescale: the running max only moves when a row's tile max exceeds
-    // it by more than 8 (log2 units), so p <= 2^8; numerator and denominator
-    // share m, so the result is exact.
-    if (__builtin_amdgcn_ballot_w64(tmax > m + 8.f)) {
-      const float mn = tmax > m + 8.f ? tmax : m;
-      const float alpha = fast_exp2(m - (mn == kNegInf ? 0.f : mn));
-      lsum *= alpha;
-#pragma unroll
-      for (int db = 0; db < NO; ++db) o[db] *= alpha;
-      m = mn;
+    for (int j = 0; j < 16; j += 2)
+      tmax = __builtin_elementwise_maximum(tmax, __builtin_elementwise_maximum(s[j], s[j + 1]));
+    {
+      auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+      tmax = __builtin_elementwise_maximum(__uint_as_float(x[0]), __uint_as_float(x[1])) * sl2;
     }
-    const float nmu = m == kNegInf ? 0.f : -m;
-    float ps = 0.f;
+    const float mn = tmax > m + 8.f ? tmax : m;
+    q.alpha = mn > m ? fast_exp2(m - mn) : 1.f;
+    m = mn;
+    q.nmu = mn == kNegInf ? 0.f : -mn;
+  };
+  auto sm_exp = [&](f32x16& s, int j0, const Soft& q) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int j = j0; j < j0 + 4; ++j) s[j] = fast_exp2(__builtin_fmaf(s[j], sl2, q.nmu));
+  };
+  auto sm_sum = [&](const f32x16& s, Soft& q) {
+    float ps4[4];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        s[kb][j] = fast_exp2(__builtin_fmaf(s[kb][j], sl2, nmu));
-        ps += s[kb][j];
-      }
-    lsum += ps;
-    const int g4 = lane >> 4, i16 = lane & 15;
+    for (int e = 0; e < 4; ++e) ps4[e] = (s[e] + s[e + 4]) + (s[e + 8] + s[e + 12]);
+    q.psum = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
+    lsum = __builtin_fmaf(lsum, q.alpha, q.psum);
+  };
+  auto sm_cvt = [&](const f32x16& s, bf16x8* pb) {
+    float pv[8];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int e = 0; e < 8; ++e) pv[e] = s[e];
+    pb[0] = to_bf16x8(pv);
 #pragma unroll
-      for (int tp = 0; tp < 2; ++tp) {
-        float pv[8];
+    for (int e = 0; e < 8; ++e) pv[e] = s[8 + e];
+    pb[1] = to_bf16x8(pv);
+  };
+  // Logical softmax piece p (0..7) of a half: max, 4 x exp, sum, convert.
+  auto sm_piece = [&](int p, f32x16& s, int k0, bool mask, Soft& q, bf16x8* pb) {
+    if (p == 0) sm_max(s, k0, mask, q);
+    else if (p <= 4) sm_exp(s, 4 * (p - 1), q);
+    else if (p == 5) sm_sum(s, q);
+    else if (p == 6) sm_cvt(s, pb);
+  };
+  // q.psum >= 0 always; testing it keeps the half's exponentials ahead of the
+  // branch, in the region where they overlap the MFMAs.
+  auto rescale = [&](const Soft& q) {
+    if (__builtin_amdgcn_ballot_w64(q.alpha != 1.f || q.psum < 0.f)) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pv[e] = s[kb][8 * tp + e];
-        const bf16x8 pb = to_bf16x8(pv);
-        const int row1 = 32 * kb + 16 * tp + 4 * h + (i16 >> 2);
-#pragma unroll
-        for (int db = 0; db < NO; ++db) {
-          const int cb = 64 * db + 32 * (g4 & 1) + 8 * (i16 & 3);  // byte column
-          const int c = cb >> 4, within = cb & 15;
-          const u32x2 r1 = lds_read_tr16(ldsV + row1 * RW + (swz<D>(row1, c) << 4) + within);
-          const u32x2 r2 = lds_read_tr16(ldsV + (row1 + 8) * RW + (swz<D>(row1 + 8, c) << 4) + within);
-          const u32x4 av = {r1[0], r1[1], r2[0], r2[1]};
-          o[db] = mfma32(as_bf16x8(av), pb, o[db]);
-        }
-      }
+      for (int db = 0; db < NO; ++db) o[db] *= q.alpha;
+    }
+  };
+  // V^T operand reads of one 16-key group (tp) and output block (db) of half kb
+  auto vread1 = [&](const char* st, int kb, int tp, int db) -> u32x4 {
+    const char* base = st + (32 * kb + 16 * tp) * RW;
+    const u32x2 r1 = lds_read_tr16(base + voff[0][db]);
+    const u32x2 r2 = lds_read_tr16(base + voff[1][db]);
+    return u32x4{r1[0], r1[1], r2[0], r2[1]};
   };
 
-  const int ntiles = (kend_wg + BN - 1) / BN;
-  gload(0);
-  lstore(0);
-  if (ntiles > 1) gload(BN);
-  __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int cur = t & 1, ts = t * BN;
-    if (wact && ts < kend_w) compute(ldsKV + cur * Cfg::kTile, ldsKV + (2 + cur) * Cfg::kTile, ts);
-    if (t + 1 < ntiles) {
-      lstore(cur ^ 1);                     // tile t+1, loaded during the previous iteration
-      if (t + 2 < ntiles) gload(ts + 2 * BN);
+  // st: the tile's stage (K at +0, V at +kTile).  The tile is scheduled by
+  // hand (sched_barrier fences keep the source order): (1) K reads, S^T of
+  // half 0, then the MFMAs of S^T half 1 each followed by two V reads of half
+  // 0 and one softmax piece of half 0; (2) the MFMAs of O^T += V^T P^T half 0,
+  // each followed by V reads and a softmax piece of half 1; (3) P V of half 1.
+  // One wave thus keeps the matrix core busy while its own VALU work runs;
+  // the two rescales of O (rare, wave-uniform branches) split the regions.
+  auto compute = [&](const char* st, int ts, bool mask, bool dma, int dts, int dstage, const uint32_t (&blk)[CHD]) {
+    f32x16 s0, s1;
+    u32x4 va0[2][NO], va1[2][NO];
+    bf16x8 pb0[2], pb1[2];
+    Soft q0, q1;
+    u32x4 ka[2][NQ];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int kk = 0; kk < NQ; ++kk) ka[kb][kk] = *reinterpret_cast<const u32x4*>(st + kb * 32 * RW + koff[kk]);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s0[j] = 0.f, s1[j] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < NQ; ++kk) s0 = mfma32(as_bf16x8(ka[0][kk]), qB[kk], s0);
+    // region 1: S^T half 1 | V reads half 0 | softmax half 0
+    constexpr int V_PER = 2 * NO / NQ;           // V operand reads (pairs) per slot
+#pragma unroll
+    for (int kk = 0; kk < NQ; ++kk) {
+      s1 = mfma32(as_bf16x8(ka[1][kk]), qB[kk], s1);
+#pragma unroll
+      for (int v = 0; v < V_PER; ++v) {
+        const int idx = kk * V_PER + v;          // (tp, db) = (idx / NO, idx % NO)
+        va0[idx / NO][idx % NO] = vread1(st, 0, idx / NO, idx % NO);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int p = kk * 8 / NQ; p < (kk + 1) * 8 / NQ; ++p) sm_piece(p, s0, ts, mask, q0, pb0);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    rescale(q0);
+    // region 2: P V half 0 | V reads half 1 | softmax half 1
+#pragma unroll
+    for (int i = 0; i < 2 * NO; ++i) {
+      const int tp = i / NO, db = i % NO;
+      o[db] = mfma32(as_bf16x8(va0[tp][db]), pb0[tp], o[db]);
+      va1[tp][db] = vread1(st, 1, tp, db);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int p = i * 8 / (2 * NO); p < (i + 1) * 8 / (2 * NO); ++p) sm_piece(p, s1, ts + 32, mask, q1, pb1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    rescale(q1);
+    // region 3: P V half 1, with the copy of a later tile spread between
+    // the MFMAs (a burst of copies right after the barrier stalls the wave)
+    static_assert(CHD <= NO, "copy instructions must fit between the P V MFMAs");
+    if (dma) {
+#pragma unroll
+      for (int i = 0; i < 2 * NO; ++i) {
+        const int tp = i / NO, db = i % NO;
+        o[db] = mfma32(as_bf16x8(va1[tp][db]), pb1[tp], o[db]);
+        if (i < 2 * CHD) dma_one(dts, dstage, blk, i / 2, i % 2);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2 * NO; ++i) {
+        const int tp = i / NO, db = i % NO;
+        o[db] = mfma32(as_bf16x8(va1[tp][db]), pb1[tp], o[db]);
+      }
+    }
+  };
+
+  // Tile t lives in stage t % NS.  Iteration t: wait for this thread's
+  // copies of tile t, barrier (tile t visible to all waves; all waves are
+  // done with tile t-1), then start the copy of tile t+NS-1 into tile t-1's
+  // stage.
+  // Tiles are taken TPB = NS / 2 at a time: one barrier per group (tile
+  // t0 .. t0+TPB-1 visible to all waves; all waves are done with the previous
+  // group).  Tile t lives in stage t % NS; its copy is spread over the P V
+  // MFMAs of tile t - TPB, into that tile's stage.
+  constexpr int TPB = NS / 2;
+  static_assert(NS % 2 == 0 && TPB >= 1, "stage ring must hold two tile groups");
+  const int ntiles = (kend_wg + BN - 1) / BN;
+  const int full_end = ctx + r0;           // tiles ending at or before key ctx + r0 need no mask
+  uint32_t nbid[CHD];
+#pragma unroll
+  for (int t = 0; t < TPB; ++t)
+    if (t < ntiles) {
+      dma_bids(t * BN, nbid);
+      dma_issue(t * BN, t, nbid);
+    }
+  if (TPB < ntiles) dma_bids(TPB * BN, nbid);
+
+  // Q as the B operand of S^T = K Q^T: lane holds Q[row n][16kk + 8h + i].
+  {
+    float x[NQ][8];
+#pragma unroll
+    for (int kk = 0; kk < NQ; ++kk) unpack_bf16x8(qraw[kk], x[kk]);
+    if (q_rope) {
+#pragma unroll
+      for (int kk = 0; kk < NQ / 2; ++kk) {
+        float c[8], sn[8];
+        unpack_bf16x8(craw[kk], c);
+        unpack_bf16x8(sraw[kk], sn);
+        rope8_bf16(x[kk], x[kk + NQ / 2], c, sn);
+      }
+    }
+#pragma unroll
+    for (int kk = 0; kk < NQ; ++kk) qB[kk] = to_bf16x8(x[kk]);
+  }
+
+  for (int t0 = 0; t0 < ntiles; t0 += TPB) {
+    wait_vmcnt<0>();                       // this thread's copies of tiles t0 .. t0+TPB-1
     __syncthreads();
+#pragma unroll
+    for (int u = 0; u < TPB; ++u) {
+      const int t = t0 + u;
+      if (t < ntiles) {
+        const int ts = t * BN;
+        const bool dma = t + TPB < ntiles;
+        const int dts = (t + TPB) * BN, dstage = (t + TPB) % NS;
+        if (wact && ts < kend_w) {
+          const char* st = lds + (t % NS) * Cfg::kStage;
+          if (DENSE || ts + BN - 1 > full_end)
+            compute(st, ts, true, dma, dts, dstage, nbid);
+          else
+            compute(st, ts, false, dma, dts, dstage, nbid);
+        } else if (dma) {
+          dma_issue(dts, dstage, nbid);
+        }
+        if (t + TPB + 1 < ntiles) dma_bids((t + TPB + 1) * BN, nbid);
+      }
+    }
   }
 
   if (row_ok) {
@@ -583,35 +754,44 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 }
 
 // ============================================================== kernels
+constexpr int kPrefillStages = 4;     // prefill LDS ring: two groups of two 64-key tiles
+
 template <int D, bool PF, bool DC, int NW> struct MixedLds {
-  static constexpr int a = PF ? PrefillCfg<D>::kLdsBytes : 0;
+  static constexpr int a = PF ? PrefillCfg<D, kPrefillStages>::kLdsBytes : 0;
   static constexpr int b = DC ? DecodeCfg<D, NW>::kLdsBytes : 0;
   static constexpr int kBytes = a > b ? a : b;
 };
 
-// Work items of both kinds in one launch (mixed continuous batch), or of one
-// kind.  Prefill workgroups are 8 waves; decode workgroups are HW x KW waves
-// (8 in a mixed launch).
+// Work items of both kinds in one launch (mixed continuous batch; 8-wave
+// workgroups), or decode items only (HW x KW waves).
 template <int D, bool PF, bool DC, int HW, int KW>
 __global__ void __launch_bounds__(64 * HW * KW) paged_attn_bf16_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[MixedLds<D, PF, DC, HW * KW>::kBytes];
   const WorkItem it = a.items[blockIdx.x];
   if (PF && (!DC || (it.kind_b & 0xff) == kItemPrefill)) {
-    if constexpr (HW * KW == kWaves) prefill_wg<D, false>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
+    if constexpr (HW * KW == kWaves) prefill_wg<D, false, kWaves, kPrefillStages>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
     return;
   }
   if constexpr (DC) decode_wg<D, HW, KW>(a, it, lds);
 }
 
+// Prefill items only.
+template <int D>
+__global__ void __launch_bounds__(64 * kWaves) prefill_bf16_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) char lds[PrefillCfg<D, kPrefillStages>::kLdsBytes];
+  const WorkItem it = a.items[blockIdx.x];
+  prefill_wg<D, false, kWaves, kPrefillStages>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
+}
+
 template <int D>
 __global__ void __launch_bounds__(64 * kWaves) dense_attn_bf16_kernel(AttnArgs a, int nwg) {
-  __shared__ __attribute__((aligned(16))) char lds[PrefillCfg<D>::kLdsBytes];
+  __shared__ __attribute__((aligned(16))) char lds[PrefillCfg<D, kPrefillStages>::kLdsBytes];
   const int w = blockIdx.x % nwg;
   const int rest = blockIdx.x / nwg;
   const int kvh = rest % a.num_kv_heads;
   const int b = rest / a.num_kv_heads;
   const WorkItem none{};
-  prefill_wg<D, true>(a, none, b, kvh, w, lds);
+  prefill_wg<D, true, kWaves, kPrefillStages>(a, none, b, kvh, w, lds);
 }
 
 template <int D, int HW, int KW>
@@ -621,7 +801,7 @@ static void launch_paged_hk(const AttnArgs& a, bool pf, bool dc, hipStream_t st)
     if constexpr (HW * KW == kWaves)
       hipLaunchKernelGGL((paged_attn_bf16_kernel<D, true, true, HW, KW>), grid, dim3(64 * kWaves), 0, st, a);
   } else if (pf) {
-    hipLaunchKernelGGL((paged_attn_bf16_kernel<D, true, false, 8, 1>), grid, dim3(64 * kWaves), 0, st, a);
+    hipLaunchKernelGGL((prefill_bf16_kernel<D>), grid, dim3(64 * kWaves), 0, st, a);
   } else {
     hipLaunchKernelGGL((paged_attn_bf16_kernel<D, false, true, HW, KW>), grid, dim3(64 * HW * KW), 0, st, a);
   }
@@ -630,7 +810,7 @@ static void launch_paged_hk(const AttnArgs& a, bool pf, bool dc, hipStream_t st)
 template <int D>
 static hipError_t launch_paged_d(const AttnArgs& a, bool pf, bool dc, hipStream_t st) {
   const int hw = a.heads_per_wg, nw = a.decode_waves;
-  if (pf && dc && nw != kWaves) return hipErrorInvalidValue;
+  if (pf && (a.prefill_waves != kWaves || (dc && nw != kWaves))) return hipErrorInvalidValue;
   if (nw == 8) {
     switch (hw) {
       case 1: launch_paged_hk<D, 1, 8>(a, pf, dc, st); break;

@@ -142,20 +142,29 @@ class AttentionPlan:
         self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         _lib.check(lib.gllm_attn_plan_upload(self._h, self.workspace.data_ptr(), nbytes,
                                              _lib.stream_ptr(self.device)))
+        arr = (ctypes.c_int64 * 9)()
+        _lib.check(lib.gllm_attn_plan_info(self._h, arr, 9))
+        keys = ("work_items", "split_tokens", "decode_seqs", "prefill_seqs", "partials", "rows", "heads_per_wg",
+                "decode_waves", "prefill_waves")
+        self._info = dict(zip(keys, list(arr)))
+        # facts every launch checks, computed once (a plan serves every layer of a step)
+        self.rows = self._info["rows"]
+        self.max_seq_len = max(sl, default=0)
+        self.table_width = -(-self.max_seq_len // block_size)
 
     @property
     def info(self) -> dict:
-        arr = (ctypes.c_int64 * 8)()
-        _lib.check(self._lib.gllm_attn_plan_info(self._h, arr, 8))
-        keys = ("work_items", "split_tokens", "decode_seqs", "prefill_seqs", "partials", "rows", "heads_per_wg",
-                "decode_waves")
-        return dict(zip(keys, list(arr)))
+        return dict(self._info)
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h is not None and h.value:
-            self._lib.gllm_attn_plan_destroy(h)
-            self._h = ctypes.c_void_p()
+        lib = getattr(self, "_lib", None)
+        if h is not None and h.value and lib is not None:
+            try:
+                lib.gllm_attn_plan_destroy(h)
+            except Exception:      # interpreter shutdown: ctypes may already be torn down
+                return
+            self._h = None
 
 
 def paged_attention(plan: AttentionPlan, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
@@ -185,12 +194,12 @@ def paged_attention(plan: AttentionPlan, q: torch.Tensor, k_cache: torch.Tensor,
         raise ValueError("block_table must be int32 [B, W] with contiguous rows")
     if block_table.shape[0] < len(plan.query_lens):
         raise ValueError("block_table has fewer rows than the plan's sequences")
-    need = max((-(-s // plan.block_size) for s in plan.seq_lens), default=0)
-    if block_table.shape[1] < need:
-        raise ValueError(f"block_table width {block_table.shape[1]} < {need} blocks the longest sequence needs")
+    if block_table.shape[1] < plan.table_width:
+        raise ValueError(f"block_table width {block_table.shape[1]} < {plan.table_width} blocks the longest "
+                         "sequence needs")
     rows = q.numel() // (Hq * D)
-    if rows < plan.info["rows"]:
-        raise ValueError(f"q has {rows} rows, the plan addresses {plan.info['rows']}")
+    if rows < plan.rows:
+        raise ValueError(f"q has {rows} rows, the plan addresses {plan.rows}")
     cos_p = sin_p = None
     rs = 0
     mode = _lib.ROPE_NONE
@@ -203,7 +212,7 @@ def paged_attention(plan: AttentionPlan, q: torch.Tensor, k_cache: torch.Tensor,
             raise ValueError("cos/sin must have contiguous rows of equal stride")
         if cos.dtype != q.dtype:
             raise ValueError("cos/sin must be in the model dtype")
-        need_rows = max(plan.seq_lens) if m == "position" else plan.info["rows"]
+        need_rows = plan.max_seq_len if m == "position" else plan.rows
         if cos.shape[0] < need_rows or cos.shape[1] < D // 2:
             raise ValueError(f"cos/sin have {cos.shape[0]} rows, {need_rows} needed")
         cos_p, sin_p, rs = cos.data_ptr(), sin.data_ptr(), cos.stride(0)

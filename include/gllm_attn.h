@@ -102,7 +102,8 @@ size_t gllm_attn_plan_workspace_bytes(const gllm_attn_plan* plan);
 int gllm_attn_plan_upload(gllm_attn_plan* plan, void* workspace, size_t workspace_bytes, void* stream);
 /* Plan facts: [0] work items, [1] split length, [2] decode-path sequences,
  * [3] prefill-path sequences, [4] split partials, [5] total query rows,
- * [6] kv heads per decode workgroup, [7] waves per decode workgroup. */
+ * [6] kv heads per decode workgroup, [7] waves per decode workgroup,
+ * [8] waves per prefill workgroup. */
 int gllm_attn_plan_info(const gllm_attn_plan* plan, int64_t* info, int32_t n);
 int gllm_attn_plan_destroy(gllm_attn_plan* plan);
 

@@ -42,6 +42,17 @@ def test_planner_host_logic():
     # seq2 (40 rows x G=4 > 16): prefill, ceil(4 * 2 row tiles / 8) = 1 workgroup x 8 kv heads
     assert (items, split, ndec, npf, parts, rows) == (1 + 16 + 8, 128, 2, 1, 8 * 16, 42)
     assert lib.gllm_attn_plan_workspace_bytes(h) > 8 * 16 * 64 * 4
+    info9 = (ctypes.c_int64 * 9)()
+    assert lib.gllm_attn_plan_info(h, info9, 9) == 0
+    assert info9[8] == 8                      # mixed launch: 8-wave prefill workgroups
+    assert lib.gllm_attn_plan_destroy(h) == 0
+    # prefill only: 100 rows x G=4 -> 4 row tiles x 4 heads = 16 waves -> 2 workgroups per kv head
+    ql = (ctypes.c_int32 * 2)(100, 33)
+    sl = (ctypes.c_int32 * 2)(100, 50)
+    assert lib.gllm_attn_plan_create(ctypes.byref(h), ql, sl, 2, 0, 32, 8, 128, 16, _lib.DTYPE_BF16, 0, 0) == 0
+    assert lib.gllm_attn_plan_info(h, info9, 9) == 0
+    assert info9[8] == 8 and info9[2] == 0 and info9[3] == 2
+    assert info9[0] == 8 * 2 + 8 * 1          # seq1: 2 row tiles x 4 heads = 8 waves -> 1 workgroup
     assert lib.gllm_attn_plan_destroy(h) == 0
 
 
