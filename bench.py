@@ -153,6 +153,30 @@ def bench_prefill(b, copies, warmup, steps, dev):
     }
 
 
+def bench_metadata(b: workloads.PagedBatch, warmup, steps, dev, cpu: bool):
+    """Device metadata builder (query-row slots + positions + cu_seqlens) on
+    one batch; with ``cpu`` also the reference path's host builder
+    (llm.py:245-293: per-row loop, left-padded slot mapping, dense 0/-inf
+    bias), restated by the oracle, on the same lengths and table."""
+    bt = b.block_table if b.block_table.is_cuda else b.block_table.to(dev)
+    sl = torch.tensor(b.seq_lens, dtype=torch.int32, device=dev)
+    ql = torch.tensor(b.q_lens, dtype=torch.int32, device=dev)
+    launches = [lambda: paged.build_metadata(bt, sl, ql, b.block_size, num_rows=b.rows)]
+    step = _graph_time(launches, warmup, steps)
+    res = {"rows": b.rows, "seqs": len(b.q_lens), "gpu_us": step * 1e3}
+    if cpu:
+        from oracle import metadata as om
+        import time
+        bt_np = bt.cpu().numpy()
+        ts = []
+        for i in range(4):
+            t0 = time.perf_counter()
+            om.build_metadata(b.ctx_lens, b.q_lens, bt_np, b.block_size, dtype=b.dtype)
+            ts.append(time.perf_counter() - t0)
+        res["cpu_reference_ms"] = statistics.median(ts[1:]) * 1e3
+    return res
+
+
 def cpu_baseline_decode(x: workloads.PagedBatch, nbytes: int):
     """The reference's CPU path for config (b): padded slot mapping + 0/-inf
     bias (llm.py:245-274), dense gather with the dtype cast (attention.py:
@@ -223,12 +247,15 @@ def main():
         b = workloads.config_b()
         head, x0, _ = bench_decode(b, args.copies, args.warmup, args.steps, args.split, dev, args.hw)
         extra["decode_1b"] = head
+        extra["metadata_decode_1b"] = bench_metadata(x0, args.warmup, args.steps, dev, not args.no_cpu)
     if "c" in cfgs:
         extra["prefill_8b"] = bench_prefill(workloads.config_c(), 2, args.warmup, args.steps, dev)
         torch.cuda.empty_cache()
     if "d" in cfgs:
-        r, _, _ = bench_decode(workloads.config_d(), 1, args.warmup, args.steps, args.split, dev, args.hw)
+        r, xd, _ = bench_decode(workloads.config_d(), 1, args.warmup, args.steps, args.split, dev, args.hw)
         extra["mixed_8b"] = r
+        extra["metadata_mixed_8b"] = bench_metadata(xd, args.warmup, args.steps, dev, False)
+        del xd
         torch.cuda.empty_cache()
     if "e" in cfgs:
         r, _, _ = bench_decode(workloads.config_e(), 1, args.warmup, max(5, args.steps // 3), args.split, dev, args.hw)

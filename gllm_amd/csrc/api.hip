@@ -71,6 +71,31 @@ extern "C" {
 const char* gllm_attn_last_error(void) { return g_last_error.c_str(); }
 int gllm_attn_version(void) { return 1; }
 
+int gllm_build_metadata(const int32_t* block_table, int64_t block_table_stride, int64_t block_table_width,
+                        const int32_t* seq_lens, const int32_t* query_lens, int32_t num_seqs,
+                        int64_t q_seq_stride, int32_t block_size, int64_t* slot_mapping, int64_t* positions,
+                        int32_t* cu_seqlens, int64_t num_rows, void* stream) {
+  if (num_seqs < 0 || num_rows < 0) return fail(GLLM_ATTN_EINVAL, "num_seqs / num_rows < 0");
+  if (num_seqs == 0) return ok();
+  if (!block_table || !seq_lens || !query_lens) return fail(GLLM_ATTN_EINVAL, "null block_table or lengths");
+  if (!slot_mapping && !positions && !cu_seqlens) return fail(GLLM_ATTN_EINVAL, "nothing to do: no output given");
+  if (block_size <= 0 || (block_size & (block_size - 1)))
+    return fail(GLLM_ATTN_EUNSUPPORTED, "block_size %d must be a power of two", block_size);
+  if (block_table_width <= 0 || block_table_stride < block_table_width)
+    return fail(GLLM_ATTN_EINVAL, "block_table width %lld / stride %lld invalid", (long long)block_table_width,
+                (long long)block_table_stride);
+  if (q_seq_stride < 0) return fail(GLLM_ATTN_EINVAL, "q_seq_stride < 0");
+  if (q_seq_stride > 0 && num_rows < (int64_t)num_seqs * q_seq_stride)
+    return fail(GLLM_ATTN_EINVAL, "num_rows %lld < num_seqs * q_seq_stride", (long long)num_rows);
+  if (cu_seqlens && q_seq_stride > 0) return fail(GLLM_ATTN_EINVAL, "cu_seqlens is for the packed layout");
+  MetadataArgs a{};
+  a.block_table = block_table; a.block_table_stride = block_table_stride; a.bt_width = block_table_width;
+  a.seq_lens = seq_lens; a.query_lens = query_lens; a.num_seqs = num_seqs; a.q_seq_stride = q_seq_stride;
+  a.block_size = block_size; a.block_shift = __builtin_ctz((unsigned)block_size);
+  a.slot_mapping = slot_mapping; a.positions = positions; a.cu_seqlens = cu_seqlens; a.num_rows = num_rows;
+  return hip_check(launch_build_metadata(a, (hipStream_t)stream), "build_metadata launch");
+}
+
 int gllm_rope_kv_write(const void* q, void* q_out, const void* k, const void* v, void* k_cache,
                        void* v_cache, const int64_t* slot_mapping, const int32_t* query_lens,
                        int64_t tokens_per_seq, const void* cos, const void* sin,

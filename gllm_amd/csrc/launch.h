@@ -78,7 +78,23 @@ struct AttnArgs {
   int32_t dtype, kv_dtype;
 };
 
+struct MetadataArgs {
+  const int32_t* block_table;
+  int64_t block_table_stride;   // elements between rows
+  int64_t bt_width;             // valid columns per row
+  const int32_t* seq_lens;
+  const int32_t* query_lens;
+  int32_t num_seqs;
+  int64_t q_seq_stride;         // > 0: padded [B, q_seq_stride] rows; 0: packed
+  int32_t block_size, block_shift;
+  int64_t* slot_mapping;        // [num_rows] (may be NULL)
+  int64_t* positions;           // [num_rows] (may be NULL)
+  int32_t* cu_seqlens;          // [num_seqs + 1], packed layout only (may be NULL)
+  int64_t num_rows;
+};
+
 hipError_t launch_rope_kv_write(const RopeKVWriteArgs& a, hipStream_t stream);
+hipError_t launch_build_metadata(const MetadataArgs& a, hipStream_t stream);
 hipError_t launch_paged_attention_bf16(const AttnArgs& a, bool has_prefill, bool has_decode, hipStream_t stream);
 hipError_t launch_dense_attention_bf16(const AttnArgs& a, int B, int Tq, hipStream_t stream);
 hipError_t launch_attention_f32(const AttnArgs& a, bool dense, int B, int max_q, hipStream_t stream);

@@ -110,6 +110,43 @@ def rope_rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     return out
 
 
+def build_metadata(block_table: torch.Tensor, seq_lens: torch.Tensor, query_lens: torch.Tensor, block_size: int,
+                   *, q_seq_stride: int = 0, num_rows: int | None = None):
+    """Query-row slot mapping and positions on the device (``gllm/llm/llm.py:
+    245-281`` without the per-row host loop or the dense bias).
+
+    ``block_table`` int32 ``[B, W]`` (contiguous rows), ``seq_lens`` /
+    ``query_lens`` int32 ``[B]`` on the same device.  ``q_seq_stride`` > 0:
+    the reference's padded ``[B, T_q]`` rows (padded rows get slot 0);
+    0: packed rows, and ``cu_seqlens`` (int32 ``[B+1]``) is returned too.
+    ``num_rows`` (packed) is the total query rows; if omitted it is read back
+    from the device (one synchronisation).  Returns
+    ``(slot_mapping int64 [rows], positions int64 [rows], cu_seqlens or None)``.
+    """
+    B = int(seq_lens.shape[0])
+    dev = block_table.device
+    for t, nm in ((seq_lens, "seq_lens"), (query_lens, "query_lens"), (block_table, "block_table")):
+        if t.dtype != torch.int32 or t.device != dev:
+            raise ValueError(f"{nm} must be int32 on {dev}")
+    if block_table.dim() != 2 or block_table.stride(1) != 1 or block_table.shape[0] < B or query_lens.shape[0] != B:
+        raise ValueError("block_table must be [B, W] with contiguous rows and lengths [B]")
+    if not seq_lens.is_contiguous() or not query_lens.is_contiguous():
+        raise ValueError("lengths must be contiguous")
+    if q_seq_stride > 0:
+        rows = B * q_seq_stride
+    else:
+        rows = int(query_lens.sum().item()) if num_rows is None else int(num_rows)
+    slots = torch.empty(rows, dtype=torch.int64, device=dev)
+    pos = torch.empty(rows, dtype=torch.int64, device=dev)
+    cu = torch.empty(B + 1, dtype=torch.int32, device=dev) if q_seq_stride == 0 else None
+    lib = _lib.load()
+    _lib.check(lib.gllm_build_metadata(block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+                                       seq_lens.data_ptr(), query_lens.data_ptr(), B, q_seq_stride, block_size,
+                                       slots.data_ptr(), pos.data_ptr(), _lib.ptr(cu), rows,
+                                       _lib.stream_ptr(dev)))
+    return slots, pos, cu
+
+
 class AttentionPlan:
     """Work plan for one batch (built once per engine step, reused by every
     layer).  Lengths are host ints, as ``gllm/llm/llm.py:233-241`` has them.

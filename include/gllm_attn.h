@@ -19,6 +19,10 @@
  *   gllm_attn_plan_*      host-side work planning for one batch (the lengths
  *                         gllm/llm/llm.py:233-241 derives), built once per
  *                         engine step and reused by every layer
+ *   gllm_build_metadata   replaces gllm/llm/llm.py:245-281 (slot mapping of the
+ *                         query rows and positions, built on the device from
+ *                         the block table and lengths instead of the per-row
+ *                         host loop; the paged kernels need no dense bias)
  *
  * Conventions: every data pointer is a device pointer the caller owns; the
  * library never allocates device memory (the paged path uses a caller-sized
@@ -56,6 +60,24 @@ typedef struct gllm_attn_plan gllm_attn_plan;
 /* Thread-local message of the last failing call ("" if none). */
 const char* gllm_attn_last_error(void);
 int gllm_attn_version(void);
+
+/*
+ * Query-row metadata on the device (gllm/llm/llm.py:245-281).  For query row
+ * r of sequence i, with c_i = seq_lens[i] - query_lens[i]:
+ *   positions[row]    = c_i + r                       (padded rows too, as llm.py:281)
+ *   slot_mapping[row] = block_table[i][(c_i+r)/bs]*bs + (c_i+r)%bs for r < query_lens[i],
+ *                       0 (the reserved dummy slot) for padded rows, as llm.py:277 gives.
+ * q_seq_stride > 0: padded layout, row = i*q_seq_stride + r for r < q_seq_stride.
+ * q_seq_stride == 0: packed rows, row = cu_seqlens[i] + r for r < query_lens[i], and
+ * cu_seqlens[0..num_seqs] (int32, optional) receives the running sums of query_lens.
+ * Rows >= num_rows are not written; block-table columns >= block_table_width
+ * (and inconsistent lengths) give slot 0.  Any output pointer may be NULL.
+ * Lengths and table are device pointers: nothing is read back to the host.
+ */
+int gllm_build_metadata(const int32_t* block_table, int64_t block_table_stride, int64_t block_table_width,
+                        const int32_t* seq_lens, const int32_t* query_lens, int32_t num_seqs,
+                        int64_t q_seq_stride, int32_t block_size, int64_t* slot_mapping, int64_t* positions,
+                        int32_t* cu_seqlens, int64_t num_rows, void* stream);
 
 /*
  * Rotate k (and, if q_out != NULL, q) with rotate-half RoPE and write k/v rows
