@@ -90,7 +90,7 @@ def _copies(b: workloads.PagedBatch, n: int, dev, on_device: bool):
     for i in range(n):
         c = workloads.PagedBatch(**{k: getattr(b, k) for k in (
             "name", "ctx_lens", "q_lens", "num_q_heads", "num_kv_heads", "head_dim", "block_size",
-            "num_blocks", "dtype", "rope_theta")})
+            "num_blocks", "dtype", "rope_theta", "kv_dtype")})
         out.append(workloads.materialize(c, dev, values_on_device=on_device, seed=2 + i))
     return out
 
@@ -248,6 +248,13 @@ def main():
         head, x0, _ = bench_decode(b, args.copies, args.warmup, args.steps, args.split, dev, args.hw)
         extra["decode_1b"] = head
         extra["metadata_decode_1b"] = bench_metadata(x0, args.warmup, args.steps, dev, not args.no_cpu)
+        # the same batch over an fp8 (e4m3fn) KV pool: half the K/V bytes
+        b8 = workloads.config_b()
+        b8.kv_dtype = torch.float8_e4m3fn
+        r8, _, _ = bench_decode(b8, args.copies, args.warmup, args.steps, args.split, dev, args.hw)
+        r8["speedup_vs_bf16_kv"] = head["ms_per_step"] / r8["ms_per_step"]
+        extra["decode_1b_fp8kv"] = r8
+        torch.cuda.empty_cache()
     if "c" in cfgs:
         extra["prefill_8b"] = bench_prefill(workloads.config_c(), 2, args.warmup, args.steps, dev)
         torch.cuda.empty_cache()

@@ -112,8 +112,9 @@ int gllm_rope_kv_write(const void* q, void* q_out, const void* k, const void* v,
   if (!kv && !q_out) return fail(GLLM_ATTN_EINVAL, "nothing to do: neither k/v nor q_out given");
   if (q_out && !q) return fail(GLLM_ATTN_EINVAL, "q_out given without q");
   if (num_kv_heads <= 0 || num_q_heads <= 0) return fail(GLLM_ATTN_EINVAL, "head counts must be > 0");
-  if (!((dtype == GLLM_DTYPE_BF16 && kv_dtype == GLLM_DTYPE_BF16) ||
-        (dtype == GLLM_DTYPE_F32 && (kv_dtype == GLLM_DTYPE_F32 || kv_dtype == GLLM_DTYPE_BF16))))
+  if (!((dtype == GLLM_DTYPE_BF16 && (kv_dtype == GLLM_DTYPE_BF16 || kv_dtype == GLLM_DTYPE_FP8_E4M3)) ||
+        (dtype == GLLM_DTYPE_F32 &&
+         (kv_dtype == GLLM_DTYPE_F32 || kv_dtype == GLLM_DTYPE_BF16 || kv_dtype == GLLM_DTYPE_FP8_E4M3))))
     return fail(GLLM_ATTN_EUNSUPPORTED, "dtype/kv_dtype combination %d/%d not supported", dtype, kv_dtype);
   const int vec = dtype == GLLM_DTYPE_F32 ? 4 : 8;
   if (head_dim <= 0 || head_dim % (2 * vec) != 0)
@@ -417,9 +418,10 @@ int gllm_paged_attention(const gllm_attn_plan* p, const void* q, int64_t q_row_s
     return fail(GLLM_ATTN_EINVAL, "rope_mode %d", rope_mode);
   if (rope_mode != GLLM_ROPE_NONE && (!rope_cos || !rope_sin || rope_row_stride < p->D / 2))
     return fail(GLLM_ATTN_EINVAL, "rope tables missing or row stride < head_dim / 2");
-  if (dtype == GLLM_DTYPE_BF16 && kv_dtype != GLLM_DTYPE_BF16)
-    return fail(GLLM_ATTN_EUNSUPPORTED, "bf16 model dtype needs a bf16 KV cache");
-  if (dtype == GLLM_DTYPE_F32 && kv_dtype != GLLM_DTYPE_F32 && kv_dtype != GLLM_DTYPE_BF16)
+  if (dtype == GLLM_DTYPE_BF16 && kv_dtype != GLLM_DTYPE_BF16 && kv_dtype != GLLM_DTYPE_FP8_E4M3)
+    return fail(GLLM_ATTN_EUNSUPPORTED, "bf16 model dtype needs a bf16 or fp8 e4m3 KV cache");
+  if (dtype == GLLM_DTYPE_F32 && kv_dtype != GLLM_DTYPE_F32 && kv_dtype != GLLM_DTYPE_BF16 &&
+      kv_dtype != GLLM_DTYPE_FP8_E4M3)
     return fail(GLLM_ATTN_EUNSUPPORTED, "kv_dtype %d", kv_dtype);
   AttnArgs a{};
   if (int rc = fill_common(a, p->Hq, p->Hkv, p->D, scale, dtype, kv_dtype)) return rc;

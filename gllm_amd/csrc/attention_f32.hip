@@ -12,6 +12,8 @@ namespace gllm {
 template <typename KV> __device__ __forceinline__ float ldkv(const KV* p);
 template <> __device__ __forceinline__ float ldkv<float>(const float* p) { return *p; }
 template <> __device__ __forceinline__ float ldkv<__bf16>(const __bf16* p) { return (float)*p; }
+// fp8 e4m3fn cache: exact widening (the reference's .to(model dtype) after the gather)
+template <> __device__ __forceinline__ float ldkv<fp8e4m3>(const fp8e4m3* p) { return __builtin_amdgcn_cvt_f32_fp8((int)p->bits, 0); }
 
 template <bool DENSE, typename KV>
 __global__ void __launch_bounds__(64) attn_f32_kernel(AttnArgs a) {
@@ -111,6 +113,8 @@ hipError_t launch_attention_f32(const AttnArgs& a, bool dense, int B, int max_q,
     hipLaunchKernelGGL((attn_f32_kernel<true, float>), grid, block, 0, st, a);
   else if (a.kv_dtype == kF32)
     hipLaunchKernelGGL((attn_f32_kernel<false, float>), grid, block, 0, st, a);
+  else if (a.kv_dtype == kFP8)
+    hipLaunchKernelGGL((attn_f32_kernel<false, fp8e4m3>), grid, block, 0, st, a);
   else
     hipLaunchKernelGGL((attn_f32_kernel<false, __bf16>), grid, block, 0, st, a);
   return hipGetLastError();

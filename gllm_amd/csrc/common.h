@@ -68,6 +68,52 @@ __device__ __forceinline__ void unpack_bf16x8(const u32x4 w, float* v) {
   }
 }
 
+// ---------------------------------------------------------------- fp8 (OCP e4m3fn)
+// Storage type of an fp8 KV cache (torch.float8_e4m3fn).  Conversions follow
+// torch's cast, checked on gfx950 against torch for all 256 codes and the
+// rounding / overflow boundaries: round to nearest even (subnormals too),
+// |x| > 464 -> NaN 0x7f|sign, 464 -> 448.  The hardware's f32 -> fp8 agrees
+// except that it gives 0xff for every NaN; torch gives 0x7f|sign (fixed up).
+struct fp8e4m3 { uint8_t bits; };
+
+__device__ __forceinline__ uint32_t fp8_nan_fix(uint32_t w, float x, int byte) {
+  if (x != x) {
+    const uint32_t code = 0x7fu | ((__float_as_uint(x) >> 24) & 0x80u);
+    w = (w & ~(0xffu << (8 * byte))) | (code << (8 * byte));
+  }
+  return w;
+}
+
+// 4 fp32 values -> 4 fp8 bytes (little-endian order a, b, c, d).
+__device__ __forceinline__ uint32_t pack_fp8x4(float a, float b, float c, float d) {
+  uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, (int)w, true);
+  if ((a != a) | (b != b) | (c != c) | (d != d)) {
+    w = fp8_nan_fix(w, a, 0);
+    w = fp8_nan_fix(w, b, 1);
+    w = fp8_nan_fix(w, c, 2);
+    w = fp8_nan_fix(w, d, 3);
+  }
+  return w;
+}
+
+// 4 fp8 bytes -> 4 fp32 (exact).
+__device__ __forceinline__ void unpack_fp8x4(uint32_t w, float* v) {
+  const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  v[0] = lo[0]; v[1] = lo[1]; v[2] = hi[0]; v[3] = hi[1];
+}
+
+// 8 fp8 bytes -> 8 bf16 (exact: every e4m3 value is a bf16 value).
+template <bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, HI));
+}
+__device__ __forceinline__ u32x4 fp8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
+  return u32x4{fp8x2_to_bf16x2<false>(w0), fp8x2_to_bf16x2<true>(w0), fp8x2_to_bf16x2<false>(w1),
+               fp8x2_to_bf16x2<true>(w1)};
+}
+
 // ---------------------------------------------------------------- memory
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }

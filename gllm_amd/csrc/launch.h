@@ -7,7 +7,7 @@
 
 namespace gllm {
 
-enum : int32_t { kF32 = 0, kBF16 = 1 };
+enum : int32_t { kF32 = 0, kBF16 = 1, kFP8 = 2 };   // kFP8: OCP e4m3fn (KV cache only)
 
 struct RopeKVWriteArgs {
   const void* q;            // [N, q_row_stride] model dtype, heads at h*D

@@ -76,9 +76,25 @@ __device__ __forceinline__ f32x4 mfma16k16(u32x2 a, u32x2 b, f32x4 c) {
 // the kv head are the 16 MFMA columns.  The KW waves of a head merge through
 // LDS; a split sequence writes (max, sum, acc) partials that merge_splits
 // combines in a second, tiny launch (no cross-workgroup fences here).
-template <int D, int HW, int KW>
+// One lane's 8 cached elements: 16 bytes of bf16, or 8 bytes of fp8 that are
+// widened (exactly) to bf16 on use.
+template <bool KV8> struct KVChunk;
+template <> struct KVChunk<false> {
+  typedef u32x4 T;
+  __device__ static T load(const char* p) { return ld16(p); }
+  __device__ static u32x4 bf16(T x) { return x; }
+};
+template <> struct KVChunk<true> {
+  typedef u32x2 T;
+  __device__ static T load(const char* p) { return *reinterpret_cast<const u32x2*>(p); }
+  __device__ static u32x4 bf16(T x) { return fp8x8_to_bf16x8(x[0], x[1]); }
+};
+
+template <int D, int HW, int KW, bool KV8>
 __device__ __forceinline__ void decode_wg(const AttnArgs& a, const WorkItem& it, char* lds) {
   constexpr int NW = HW * KW;
+  constexpr int E = KV8 ? 1 : 2;   // bytes per cached element
+  using KC = KVChunk<KV8>;
   using Cfg = DecodeCfg<D, NW>;
   constexpr int NK = D / 32;   // 32-dim K chunks per key
   constexpr int ND = D / 16;   // 16-dim output blocks
@@ -142,9 +158,9 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, const WorkItem& it,
   __syncthreads();
 
   // byte addressing: slot (< 2^32) x slot bytes (< 2^32) is one 32x32->64 mad
-  const uint32_t sbytes = (uint32_t)(a.cache_slot_stride * 2);
-  const char* kc = (const char*)a.k_cache + ((int64_t)(head_ok ? kvh : 0) * D + 8 * grp) * 2;
-  const char* vc = (const char*)a.v_cache + ((int64_t)(head_ok ? kvh : 0) * D + 8 * grp) * 2;
+  const uint32_t sbytes = (uint32_t)(a.cache_slot_stride * E);
+  const char* kc = (const char*)a.k_cache + ((int64_t)(head_ok ? kvh : 0) * D + 8 * grp) * E;
+  const char* vc = (const char*)a.v_cache + ((int64_t)(head_ok ? kvh : 0) * D + 8 * grp) * E;
   const float sl2 = a.scale * kLog2e;
   char* ldsV = lds + wave * Cfg::kVBytes;
   const uint32_t bmask = a.block_size - 1;
@@ -156,26 +172,26 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, const WorkItem& it,
 
   // this wave's sub-tiles: j = ki + KW * t, t < ntw
   const int ntw = head_ok && nsub > ki ? (nsub - ki + KW - 1) / KW : 0;
-  u32x4 kr[PF + 1][NK], vr[PF + 1][NK];
-  auto issue = [&](int t, u32x4 (&kd)[NK], u32x4 (&vd)[NK]) {
+  typename KC::T kr[PF + 1][NK], vr[PF + 1][NK];
+  auto issue = [&](int t, typename KC::T (&kd)[NK], typename KC::T (&vd)[NK]) {
     const int key = min(kbeg + 16 * (ki + KW * t) + n, kend - 1);
     const uint32_t slot = (uint32_t)lbid[(key >> a.block_shift) - blk0] * (uint32_t)a.block_size + ((uint32_t)key & bmask);
     const uint64_t off = (uint64_t)slot * sbytes;
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
-      kd[kk] = ld16(kc + off + 64 * kk);
-      vd[kk] = ld16(vc + off + 64 * kk);
+      kd[kk] = KC::load(kc + off + 32 * E * kk);
+      vd[kk] = KC::load(vc + off + 32 * E * kk);
     }
   };
-  auto compute = [&](int t, const u32x4 (&kd)[NK], const u32x4 (&vd)[NK]) {
+  auto compute = [&](int t, const typename KC::T (&kd)[NK], const typename KC::T (&vd)[NK]) {
     // tiles past the last one (ring padding) are fully masked
     const int kb = t < ntw ? kbeg + 16 * (ki + KW * t) : kend;
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) s = mfma16(as_bf16x8(kd[kk]), qB[kk], s);
+    for (int kk = 0; kk < NK; ++kk) s = mfma16(as_bf16x8(KC::bf16(kd[kk])), qB[kk], s);
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk)
-      *reinterpret_cast<u32x4*>(ldsV + n * RB + (32 * kk + 8 * grp) * 2) = vd[kk];
+      *reinterpret_cast<u32x4*>(ldsV + n * RB + (32 * kk + 8 * grp) * 2) = KC::bf16(vd[kk]);
     // lane holds S[key kb + 4grp + j][row n]
     float p[4];
 #pragma unroll
@@ -368,8 +384,9 @@ __device__ __forceinline__ int pf_swz(int r) {
 // Paged mode: keys through the block table, causal mask on diagonal tiles
 // only.  Dense mode (DENSE): keys from k/v [B, T, Hkv, D], additive bias
 // [B, T_q, T] on every tile.
-template <int D, bool DENSE, int NW, int NS>
+template <int D, bool DENSE, int NW, int NS, bool KV8>
 __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it, int seq, int kvh, int wgrp, char* lds) {
+  static_assert(!(DENSE && KV8), "the dense op has no cache");
   using Cfg = PrefillCfg<D, NS>;
   constexpr int NQ = D / 16;               // Q operand chunks (16 dims)
   constexpr int NO = D / 32;               // output blocks (32 dims)
@@ -469,7 +486,8 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   constexpr int NSEG = BN / RPS;
   constexpr int CHD = NSEG / NW;          // copies per wave per K (or V) tile
   static_assert(CHD >= 1 && NSEG % NW == 0, "tile / workgroup mismatch");
-  const uint32_t sbytes = (uint32_t)(a.cache_slot_stride * 2);
+  constexpr int E = KV8 ? 1 : 2;           // bytes per cached element
+  const uint32_t sbytes = (uint32_t)(a.cache_slot_stride * E);
   const uint32_t bmask = a.block_size - 1;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
   // Block ids of the DMA rows of the tile starting at key ts (fetched one
@@ -491,31 +509,53 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
       }
     }
   };
-  // One copy instruction: chunk row set i of the tile at key ts, K (v = 0)
-  // or V (v = 1), into `stage`.
-  auto dma_one = [&](int ts, int stage, const uint32_t (&blk)[CHD], int i, int v) {
+  // Source of one lane's 8 elements (logical chunk lc of its row) for copy
+  // instruction i, K (v = 0) or V (v = 1), of the tile at key ts.
+  auto copy_src = [&](int ts, const uint32_t (&blk)[CHD], int i, int v) -> const char* {
     const int sg = i * NW + wave;
     const int row = sg * RPS + lane / CPR;
     const int lc = (lane % CPR) ^ pf_swz<D>(row);
     const int p = min(ts + row, kend_wg - 1);
-    const char* src;
     if (DENSE) {
-      src = v ? (const char*)a.v + ((int64_t)seq * a.v_batch_stride + (int64_t)p * a.v_row_stride + (int64_t)kvh * D) * 2
-              : (const char*)a.k + ((int64_t)seq * a.k_batch_stride + (int64_t)p * a.k_row_stride + (int64_t)kvh * D) * 2;
-    } else {
-      const uint64_t off = (uint64_t)(blk[i] * (uint32_t)a.block_size + ((uint32_t)p & bmask)) * sbytes +
-                           (uint64_t)kvh * D * 2;
-      src = (const char*)(v ? a.v_cache : a.k_cache) + off;
+      return (v ? (const char*)a.v + ((int64_t)seq * a.v_batch_stride + (int64_t)p * a.v_row_stride + (int64_t)kvh * D) * 2
+                : (const char*)a.k + ((int64_t)seq * a.k_batch_stride + (int64_t)p * a.k_row_stride + (int64_t)kvh * D) * 2) +
+             lc * 16;
     }
+    const uint64_t off = (uint64_t)(blk[i] * (uint32_t)a.block_size + ((uint32_t)p & bmask)) * sbytes +
+                         (uint64_t)kvh * D * E;
+    return (const char*)(v ? a.v_cache : a.k_cache) + off + lc * 8 * E;
+  };
+  // One copy instruction into `stage`: bf16 caches go HBM -> LDS directly;
+  // fp8 caches are fetched into registers (`fp8_fetch`, a tile ahead) and
+  // widened to bf16 when written (`fp8_put`), so LDS always holds bf16.
+  auto dma_one = [&](int ts, int stage, const uint32_t (&blk)[CHD], int i, int v) {
+    const int sg = i * NW + wave;
     const uint32_t dst = __builtin_amdgcn_readfirstlane(lds0 + stage * Cfg::kStage + v * Cfg::kTile + sg * 1024);
-    lds_dma16(src + lc * 16, dst);
+    lds_dma16(copy_src(ts, blk, i, v), dst);
+  };
+  u32x2 f8st[CHD][2];                      // fp8 cache: fetched chunks of the tile being copied
+  auto fp8_fetch = [&](int ts, const uint32_t (&blk)[CHD]) {
+#pragma unroll
+    for (int i = 0; i < CHD; ++i)
+#pragma unroll
+      for (int v = 0; v < 2; ++v) f8st[i][v] = *reinterpret_cast<const u32x2*>(copy_src(ts, blk, i, v));
+  };
+  auto fp8_put = [&](int stage, int i, int v) {
+    const int sg = i * NW + wave;
+    *reinterpret_cast<u32x4*>(lds + stage * Cfg::kStage + v * Cfg::kTile + sg * 1024 + lane * 16) =
+        fp8x8_to_bf16x8(f8st[i][v][0], f8st[i][v][1]);
   };
   auto dma_issue = [&](int ts, int stage, const uint32_t (&blk)[CHD]) {
+    if (KV8) fp8_fetch(ts, blk);
 #pragma unroll
-    for (int i = 0; i < CHD; ++i) {
-      dma_one(ts, stage, blk, i, 0);
-      dma_one(ts, stage, blk, i, 1);
-    }
+    for (int i = 0; i < CHD; ++i)
+#pragma unroll
+      for (int v = 0; v < 2; ++v) {
+        if (KV8)
+          fp8_put(stage, i, v);
+        else
+          dma_one(ts, stage, blk, i, v);
+      }
   };
 
   const float sl2 = a.scale * kLog2e;
@@ -664,7 +704,12 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
       for (int i = 0; i < 2 * NO; ++i) {
         const int tp = i / NO, db = i % NO;
         o[db] = mfma32(as_bf16x8(va1[tp][db]), pb1[tp], o[db]);
-        if (i < 2 * CHD) dma_one(dts, dstage, blk, i / 2, i % 2);
+        if (i < 2 * CHD) {
+          if (KV8)
+            fp8_put(dstage, i / 2, i % 2);     // fetched at the start of the tile
+          else
+            dma_one(dts, dstage, blk, i / 2, i % 2);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
@@ -725,6 +770,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
         const int ts = t * BN;
         const bool dma = t + TPB < ntiles;
         const int dts = (t + TPB) * BN, dstage = (t + TPB) % NS;
+        if (KV8 && dma && wact && ts < kend_w) fp8_fetch(dts, nbid);   // written in the tile's last region
         if (wact && ts < kend_w) {
           const char* st = lds + (t % NS) * Cfg::kStage;
           if (DENSE || ts + BN - 1 > full_end)
@@ -764,23 +810,24 @@ template <int D, bool PF, bool DC, int NW> struct MixedLds {
 
 // Work items of both kinds in one launch (mixed continuous batch; 8-wave
 // workgroups), or decode items only (HW x KW waves).
-template <int D, bool PF, bool DC, int HW, int KW>
+template <int D, bool PF, bool DC, int HW, int KW, bool KV8>
 __global__ void __launch_bounds__(64 * HW * KW) paged_attn_bf16_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[MixedLds<D, PF, DC, HW * KW>::kBytes];
   const WorkItem it = a.items[blockIdx.x];
   if (PF && (!DC || (it.kind_b & 0xff) == kItemPrefill)) {
-    if constexpr (HW * KW == kWaves) prefill_wg<D, false, kWaves, kPrefillStages>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
+    if constexpr (HW * KW == kWaves)
+      prefill_wg<D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
     return;
   }
-  if constexpr (DC) decode_wg<D, HW, KW>(a, it, lds);
+  if constexpr (DC) decode_wg<D, HW, KW, KV8>(a, it, lds);
 }
 
 // Prefill items only.
-template <int D>
+template <int D, bool KV8>
 __global__ void __launch_bounds__(64 * kWaves) prefill_bf16_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[PrefillCfg<D, kPrefillStages>::kLdsBytes];
   const WorkItem it = a.items[blockIdx.x];
-  prefill_wg<D, false, kWaves, kPrefillStages>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
+  prefill_wg<D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
 }
 
 template <int D>
@@ -791,32 +838,32 @@ __global__ void __launch_bounds__(64 * kWaves) dense_attn_bf16_kernel(AttnArgs a
   const int kvh = rest % a.num_kv_heads;
   const int b = rest / a.num_kv_heads;
   const WorkItem none{};
-  prefill_wg<D, true, kWaves, kPrefillStages>(a, none, b, kvh, w, lds);
+  prefill_wg<D, true, kWaves, kPrefillStages, false>(a, none, b, kvh, w, lds);
 }
 
-template <int D, int HW, int KW>
+template <int D, int HW, int KW, bool KV8>
 static void launch_paged_hk(const AttnArgs& a, bool pf, bool dc, hipStream_t st) {
   dim3 grid(a.n_items);
   if (pf && dc) {
     if constexpr (HW * KW == kWaves)
-      hipLaunchKernelGGL((paged_attn_bf16_kernel<D, true, true, HW, KW>), grid, dim3(64 * kWaves), 0, st, a);
+      hipLaunchKernelGGL((paged_attn_bf16_kernel<D, true, true, HW, KW, KV8>), grid, dim3(64 * kWaves), 0, st, a);
   } else if (pf) {
-    hipLaunchKernelGGL((prefill_bf16_kernel<D>), grid, dim3(64 * kWaves), 0, st, a);
+    hipLaunchKernelGGL((prefill_bf16_kernel<D, KV8>), grid, dim3(64 * kWaves), 0, st, a);
   } else {
-    hipLaunchKernelGGL((paged_attn_bf16_kernel<D, false, true, HW, KW>), grid, dim3(64 * HW * KW), 0, st, a);
+    hipLaunchKernelGGL((paged_attn_bf16_kernel<D, false, true, HW, KW, KV8>), grid, dim3(64 * HW * KW), 0, st, a);
   }
 }
 
-template <int D>
+template <int D, bool KV8>
 static hipError_t launch_paged_d(const AttnArgs& a, bool pf, bool dc, hipStream_t st) {
   const int hw = a.heads_per_wg, nw = a.decode_waves;
   if (pf && (a.prefill_waves != kWaves || (dc && nw != kWaves))) return hipErrorInvalidValue;
   if (nw == 8) {
     switch (hw) {
-      case 1: launch_paged_hk<D, 1, 8>(a, pf, dc, st); break;
-      case 2: launch_paged_hk<D, 2, 4>(a, pf, dc, st); break;
-      case 4: launch_paged_hk<D, 4, 2>(a, pf, dc, st); break;
-      case 8: launch_paged_hk<D, 8, 1>(a, pf, dc, st); break;
+      case 1: launch_paged_hk<D, 1, 8, KV8>(a, pf, dc, st); break;
+      case 2: launch_paged_hk<D, 2, 4, KV8>(a, pf, dc, st); break;
+      case 4: launch_paged_hk<D, 4, 2, KV8>(a, pf, dc, st); break;
+      case 8: launch_paged_hk<D, 8, 1, KV8>(a, pf, dc, st); break;
       default: return hipErrorInvalidValue;
     }
   } else {
@@ -830,8 +877,12 @@ static hipError_t launch_paged_d(const AttnArgs& a, bool pf, bool dc, hipStream_
 
 hipError_t launch_paged_attention_bf16(const AttnArgs& a, bool has_prefill, bool has_decode, hipStream_t st) {
   if (a.n_items == 0) return hipSuccess;
-  if (a.head_dim == 64) return launch_paged_d<64>(a, has_prefill, has_decode, st);
-  if (a.head_dim == 128) return launch_paged_d<128>(a, has_prefill, has_decode, st);
+  const bool kv8 = a.kv_dtype == kFP8;
+  if (!kv8 && a.kv_dtype != kBF16) return hipErrorInvalidValue;
+  if (a.head_dim == 64)
+    return kv8 ? launch_paged_d<64, true>(a, has_prefill, has_decode, st) : launch_paged_d<64, false>(a, has_prefill, has_decode, st);
+  if (a.head_dim == 128)
+    return kv8 ? launch_paged_d<128, true>(a, has_prefill, has_decode, st) : launch_paged_d<128, false>(a, has_prefill, has_decode, st);
   return hipErrorInvalidValue;
 }
 

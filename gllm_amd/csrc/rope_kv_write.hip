@@ -1,4 +1,5 @@
-// Fused rotate-half RoPE + paged KV-cache write.
+// Fused rotate-half RoPE + paged KV-cache write (cache in the model dtype,
+// bf16 under an fp32 model, or fp8 e4m3fn).
 //
 // Replaces gllm/model/layers/attention.py:151-161 (apply_rope on k, the
 // index_put_ of k/v through query_slot_mapping) and, optionally, the q half
@@ -53,6 +54,15 @@ template <> __device__ void store_vals<__bf16>(void* p, const float* v, int n) {
     u32x2 w;
     for (int i = 0; i < 2; ++i) w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
     st8(p, w);
+  }
+}
+
+// fp8 cache: the model-dtype values are cast like torch's .to(float8_e4m3fn).
+template <> __device__ void store_vals<fp8e4m3>(void* p, const float* v, int n) {
+  if (n == 8) {
+    st8(p, u32x2{pack_fp8x4(v[0], v[1], v[2], v[3]), pack_fp8x4(v[4], v[5], v[6], v[7])});
+  } else {  // n == 4
+    *reinterpret_cast<uint32_t*>(p) = pack_fp8x4(v[0], v[1], v[2], v[3]);
   }
 }
 
@@ -138,6 +148,10 @@ hipError_t launch_rope_kv_write(const RopeKVWriteArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((rope_kv_write_kernel<float, float>), grid, block, 0, stream, a);
   else if (a.dtype == kF32 && a.kv_dtype == kBF16)
     hipLaunchKernelGGL((rope_kv_write_kernel<float, __bf16>), grid, block, 0, stream, a);
+  else if (a.dtype == kBF16 && a.kv_dtype == kFP8)
+    hipLaunchKernelGGL((rope_kv_write_kernel<__bf16, fp8e4m3>), grid, block, 0, stream, a);
+  else if (a.dtype == kF32 && a.kv_dtype == kFP8)
+    hipLaunchKernelGGL((rope_kv_write_kernel<float, fp8e4m3>), grid, block, 0, stream, a);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

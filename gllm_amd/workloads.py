@@ -26,6 +26,7 @@ class PagedBatch:
     num_blocks: int
     dtype: torch.dtype
     rope_theta: float | None = None
+    kv_dtype: torch.dtype | None = None      # KV cache dtype (None: the model dtype)
     # filled by materialize()
     q: torch.Tensor | None = None            # [rows, Hq, D] (packed rows)
     k_new: torch.Tensor | None = None        # [rows, Hkv, D] new tokens' K (pre-RoPE)
@@ -47,7 +48,8 @@ class PagedBatch:
         return sum(self.q_lens)
 
     def kv_bytes_per_token(self) -> int:
-        return 2 * self.num_kv_heads * self.head_dim * torch.finfo(self.dtype).bits // 8
+        kv = self.kv_dtype or self.dtype
+        return 2 * self.num_kv_heads * self.head_dim * kv.itemsize
 
 
 def block_tables(seq_lens, block_size, num_blocks, seed=1):
@@ -91,6 +93,8 @@ def materialize(b: PagedBatch, device, values_on_device: bool = False, seed: int
         b.k_cache, b.v_cache = mk(nslots, Hkv, D), mk(nslots, Hkv, D)
         b.q, b.k_new, b.v_new = b.q.to(device), b.k_new.to(device), b.v_new.to(device)
         b.k_cache, b.v_cache = b.k_cache.to(device), b.v_cache.to(device)
+    if b.kv_dtype is not None and b.kv_dtype != b.dtype:      # e.g. an fp8 pool: torch's cast of the draws
+        b.k_cache, b.v_cache = b.k_cache.to(b.kv_dtype), b.v_cache.to(b.kv_dtype)
     b.block_table = bt.to(device)
     starts, slots = [], []
     r = 0

@@ -47,7 +47,7 @@ enum {
   GLLM_ATTN_EHIP = 3          /* HIP runtime error */
 };
 
-enum { GLLM_DTYPE_F32 = 0, GLLM_DTYPE_BF16 = 1 };
+enum { GLLM_DTYPE_F32 = 0, GLLM_DTYPE_BF16 = 1, GLLM_DTYPE_FP8_E4M3 = 2 /* torch.float8_e4m3fn, KV cache only */ };
 
 enum {
   GLLM_ROPE_NONE = 0,        /* q already rotated */
@@ -87,7 +87,9 @@ int gllm_build_metadata(const int32_t* block_table, int64_t block_table_stride, 
  * t / tokens_per_seq and rows past query_lens[seq] (the reference's padded
  * rows, which it sends to dummy slot 0) are skipped.  Slots outside
  * [0, num_slots) are never written.  cos/sin rows: rope_rows[t] if given,
- * else t.  dtype is the model dtype of q/k/v/cos/sin; kv_dtype the cache's.
+ * else t.  dtype is the model dtype of q/k/v/cos/sin; kv_dtype the cache's
+ * (the model dtype, bf16 under f32, or fp8 e4m3fn: rounded like torch's
+ * .to(torch.float8_e4m3fn), NaN -> 0x7f|sign, |x| > 464 -> NaN).
  * Every op is rounded to the model dtype in the reference's order, so the
  * written K/V are bit-identical to attention.py:151-161.  With k == v == NULL
  * only q is rotated into q_out (Attention.apply_rope on one tensor).
@@ -139,8 +141,11 @@ int gllm_attn_plan_destroy(gllm_attn_plan* plan);
  * Key p of sequence i is visible to query row r iff p <= c_i + r.
  * Query head h reads kv head h / (num_q_heads / num_kv_heads).
  * rope_mode != NONE rotates q on load (bit-identical to apply_rope).
- * bf16/bf16 runs the MFMA kernels (head_dim 64 or 128); f32 model dtype runs
- * the fp32 kernel (kv f32 or bf16).  Returns after enqueueing on `stream`.
+ * bf16 model dtype runs the MFMA kernels (head_dim 64 or 128) over a bf16 or
+ * fp8 e4m3fn cache; f32 model dtype runs the fp32 kernel (kv f32, bf16 or
+ * fp8 e4m3fn).  An fp8 cache is read as the reference reads it: each value
+ * widened exactly to the model dtype (attention.py:169-170's .to(q.dtype)).
+ * Returns after enqueueing on `stream`.
  */
 int gllm_paged_attention(const gllm_attn_plan* plan, const void* q, int64_t q_row_stride,
                          void* out, int64_t out_row_stride, const void* k_cache,

@@ -19,14 +19,18 @@ DEV = "cuda"
 
 
 def _bits(t):
-    return t.cpu().contiguous().view(torch.int16 if t.element_size() == 2 else torch.int32)
+    return t.cpu().contiguous().view({1: torch.uint8, 2: torch.int16, 4: torch.int32}[t.element_size()])
 
 
 # ------------------------------------------------------------ (a) RoPE + KV write
 @pytest.mark.parametrize("dtype,kv_dtype,D", [(torch.bfloat16, torch.bfloat16, 64),
                                               (torch.bfloat16, torch.bfloat16, 128),
                                               (torch.float32, torch.float32, 64),
-                                              (torch.float32, torch.bfloat16, 128)])
+                                              (torch.float32, torch.bfloat16, 128),
+                                              # fp8 cache: the write must round like torch's .to(float8_e4m3fn)
+                                              (torch.bfloat16, torch.float8_e4m3fn, 64),
+                                              (torch.bfloat16, torch.float8_e4m3fn, 128),
+                                              (torch.float32, torch.float8_e4m3fn, 64)])
 def test_rope_kv_write_bit_exact(dtype, kv_dtype, D):
     print(f"rope_kv_write dtype={dtype} kv={kv_dtype} D={D}", flush=True)
     g = torch.Generator().manual_seed(10 + D)
@@ -64,6 +68,29 @@ def test_rope_kv_write_bit_exact(dtype, kv_dtype, D):
     # apply_rope drop-in on a whole tensor
     qr = paged.rope_rotate(q.to(DEV), cos.to(DEV), sin.to(DEV))
     assert torch.equal(_bits(qr), _bits(q_ref))
+
+
+def test_fp8_cache_cast_exhaustive():
+    """Every bf16 bit pattern (NaN, inf, subnormals, overflow included) and a
+    set of fp32 values written to an fp8 cache through the V path: bytes equal
+    torch's .to(float8_e4m3fn) (the reference's write, attention.py:161)."""
+    Hkv, D = 1, 64
+    allb = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).reshape(-1, Hkv, D)
+    g = torch.Generator().manual_seed(77)
+    f32 = torch.cat([torch.randn(59968, generator=g) * 300, torch.tensor(
+        [464.0, 463.99, 464.01, 448.0, 480.0, -464.0, 2 ** -10, 3 * 2 ** -10, 2 ** -6, 2 ** -6 * 0.999,
+         float("inf"), float("-inf"), float("nan"), -float("nan"), 0.0, -0.0] * 4)]).reshape(-1, Hkv, D)
+    for v in (allb, f32):
+        n = v.shape[0]
+        k = torch.zeros_like(v)
+        cos = torch.ones(n, D // 2, dtype=v.dtype)
+        sin = torch.zeros(n, D // 2, dtype=v.dtype)
+        kc = torch.zeros(n, Hkv, D, dtype=torch.float8_e4m3fn, device=DEV)
+        vc = torch.zeros(n, Hkv, D, dtype=torch.float8_e4m3fn, device=DEV)
+        slots = torch.arange(n, dtype=torch.int64)
+        paged.rope_kv_write(k.to(DEV), v.to(DEV), cos.to(DEV), sin.to(DEV), kc, vc, slots.to(DEV))
+        torch.cuda.synchronize()
+        assert torch.equal(vc.cpu().view(torch.uint8), v.to(torch.float8_e4m3fn).view(torch.uint8)), v.dtype
 
 
 # ------------------------------------------------------------ (b) decode
