@@ -58,13 +58,109 @@ struct gllm_attn_plan {
   int64_t n_partials = 0;
   std::vector<SeqInfo> seqs;
   std::vector<WorkItem> items;
+  // page-balanced decode: workgroup w runs segs[seg_ptr[w] .. seg_ptr[w + 1])
+  std::vector<DecodeSeg> segs;
+  std::vector<int32_t> seg_ptr;
   // staging copy of [items | seqs] in pinned host memory, device offsets
   void* pinned = nullptr;
   bool pinned_is_host_malloc = false;  // hipHostMalloc unavailable (no device): plain malloc
-  size_t off_items = 0, off_seqs = 0, off_ctr = 0, off_ml = 0, off_part = 0, ws_bytes = 0;
+  size_t off_items = 0, off_seqs = 0, off_segs = 0, off_segptr = 0, off_ctr = 0, off_ml = 0, off_part = 0, ws_bytes = 0;
   char* ws = nullptr;
   hipEvent_t upload_done = nullptr;
 };
+
+namespace {
+
+// Resident 8-wave decode workgroups per CU (register-bound: 2 at D = 64,
+// 1 at D = 128).
+#ifndef GLLM_DECODE_WG_PER_CU
+#define GLLM_DECODE_WG_PER_CU(D) ((D) == 64 ? 2 : 1)
+#endif
+
+// Page-balanced decode plan (decode-only batches): the batch's keys, in
+// 16-key units per (sequence, kv-head group), are dealt out as equal
+// contiguous ranges to one workgroup per resident slot, so every
+// CU streams the same number of bytes whatever the spread of sequence
+// lengths.  A workgroup's range becomes one segment per (sequence, group) it
+// touches (cut further so a segment caches at most 511 block ids).  A
+// (sequence, group) with several segments writes partials; the workgroup
+// drawing its last ticket merges them in the same launch.  HW: the largest
+// of 8, 4, 2, 1 that divides Hkv, so the 8 waves read all HW heads of a slot
+// (HW x D x 2 contiguous bytes) together.
+// Units (16 keys x one kv-head group) and workgroups of a page-balanced plan.
+struct BalancedShape {
+  int hw, hgroups;
+  int64_t units, wgs;
+};
+BalancedShape balanced_shape(const gllm_attn_plan* p, int cus, int heads_req) {
+  BalancedShape b{};
+  b.hw = heads_req;
+  if (!b.hw) {
+    b.hw = 8;
+    while (b.hw > 1 && p->Hkv % b.hw) b.hw /= 2;
+  }
+  b.hgroups = (p->Hkv + b.hw - 1) / b.hw;
+  for (const SeqInfo& si : p->seqs) b.units += (int64_t)b.hgroups * ((si.ctx_len + si.q_len + 15) / 16);
+  b.wgs = std::max<int64_t>(1, std::min<int64_t>(b.units, (int64_t)cus * GLLM_DECODE_WG_PER_CU(p->D)));
+  return b;
+}
+
+// Page-balanced plans pay a partial write, an L2 write-back (agent-scope
+// release) and a ticket per segment, and the merges of the last segments
+// sit on the launch's tail: measured on MI355X this wins when a workgroup
+// streams at least ~2048 keys (long-context batches) and loses to the
+// split planner below that.
+constexpr int64_t kBalancedMinUnitsPerWg = 128;
+
+void plan_balanced_decode(gllm_attn_plan* p, int cus, int heads_req) {
+  const BalancedShape shape = balanced_shape(p, cus, heads_req);
+  const int hw = shape.hw, hgroups = shape.hgroups;
+  const int64_t bs = p->bs;
+  const int64_t ucap = std::max<int64_t>(1, (bs <= 16 ? 512 * bs : 510 * bs) / 16);
+  const int64_t U = shape.units, W = shape.wgs;
+  p->heads_per_wg = hw;
+  p->decode_waves = 8;
+  p->split_len = 0;
+  p->n_decode_seqs = p->num_seqs;
+  p->segs.clear();
+  p->seg_ptr.assign((size_t)W + 1, 0);
+  std::vector<int32_t> seg_wg;
+  int64_t u0 = 0, j = 0;
+  for (int i = 0; i < p->num_seqs; ++i) {
+    SeqInfo& si = p->seqs[i];
+    si.nsplits = 1;
+    const int L = si.ctx_len + si.q_len;
+    const int64_t nu = (L + 15) / 16;
+    for (int hg = 0; hg < hgroups; ++hg) {
+      const size_t first = p->segs.size();
+      for (int64_t u = 0; u < nu;) {
+        while (U * (j + 1) / W <= u0 + u) ++j;        // workgroup owning unit u0 + u
+        const int64_t take = std::min(std::min(nu - u, U * (j + 1) / W - (u0 + u)), ucap);
+        DecodeSeg sg{};
+        sg.seq = i; sg.hg = hg;
+        sg.k0 = (int32_t)(16 * u);
+        sg.k1 = (int32_t)std::min<int64_t>(L, 16 * (u + take));
+        sg.q_row_start = si.q_row_start; sg.ctx_len = si.ctx_len; sg.q_len = si.q_len;
+        sg.ticket = i * hgroups + hg;
+        p->segs.push_back(sg);
+        seg_wg.push_back((int32_t)j);
+        u += take;
+      }
+      u0 += nu;
+      const int nseg = (int)(p->segs.size() - first);
+      const int32_t pbase = (int32_t)p->n_partials;
+      if (nseg > 1) p->n_partials += (int64_t)hw * nseg;
+      for (int k = 0; k < nseg; ++k) {
+        DecodeSeg& sg = p->segs[first + k];
+        sg.nseg = nseg; sg.ord = k; sg.pbase = nseg > 1 ? pbase : 0;
+      }
+    }
+  }
+  for (int32_t w : seg_wg) ++p->seg_ptr[(size_t)w + 1];
+  for (int64_t w = 0; w < W; ++w) p->seg_ptr[(size_t)w + 1] += p->seg_ptr[(size_t)w];
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -158,7 +254,8 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
   } else {
     return fail(GLLM_ATTN_EUNSUPPORTED, "dtype %d", dtype);
   }
-  if (split_tokens < 0 || split_tokens % 32) return fail(GLLM_ATTN_EINVAL, "split_tokens must be a multiple of 32");
+  if (split_tokens != GLLM_SPLIT_BALANCED && (split_tokens < 0 || split_tokens % 32))
+    return fail(GLLM_ATTN_EINVAL, "split_tokens must be a multiple of 32 or GLLM_SPLIT_BALANCED");
   if (decode_heads_per_wg != 0 && decode_heads_per_wg != 1 && decode_heads_per_wg != 2 &&
       decode_heads_per_wg != 4 && decode_heads_per_wg != 8)
     return fail(GLLM_ATTN_EINVAL, "decode_heads_per_wg must be 0 (auto), 1, 2, 4 or 8");
@@ -204,6 +301,22 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
       cus = prop.multiProcessorCount;
     else
       (void)hipGetLastError();
+    int64_t n_pf = 0;
+    for (int i = 0; i < num_seqs; ++i)
+      if ((int64_t)query_lens[i] * G > 16) ++n_pf;
+    if (split_tokens == GLLM_SPLIT_BALANCED && n_pf > 0) {
+      delete p;
+      return fail(GLLM_ATTN_EINVAL, "GLLM_SPLIT_BALANCED plans decode-only batches (%lld prefill-path sequences)",
+                  (long long)n_pf);
+    }
+    bool balanced = split_tokens == GLLM_SPLIT_BALANCED && num_seqs > 0;
+    if (n_pf == 0 && split_tokens == 0 && num_seqs > 0) {
+      const BalancedShape bsh = balanced_shape(p, cus, decode_heads_per_wg);
+      balanced = bsh.units >= kBalancedMinUnitsPerWg * bsh.wgs;
+    }
+    if (balanced) {
+      plan_balanced_decode(p, cus, decode_heads_per_wg);
+    } else {
     // Decode: one 8-wave workgroup per (sequence, split, HW kv heads); the
     // other 8 / HW waves interleave each head's keys.  Rule (fitted to MI355X
     // measurements of the benchmark batches): the first HW of 2, 1, 4, 8
@@ -231,7 +344,7 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
     if (!fills) best_hw = decode_heads_per_wg ? decode_heads_per_wg : 2;
     while (best_hw > 1 && best_hw / 2 >= num_kv_heads) best_hw /= 2;  // no idle head slots
     const int best_nw = 8;
-    int64_t best_S = split_tokens;
+    int64_t best_S = split_tokens < 0 ? 0 : split_tokens;
     if (best_S == 0) {
       if (fills) {
         best_S = cap;
@@ -315,12 +428,20 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
       delete p;
       return fail(GLLM_ATTN_EINVAL, "too many work items");
     }
+    }
+  }
+  if (p->n_partials > (int64_t)INT32_MAX / 16) {
+    delete p;
+    return fail(GLLM_ATTN_EINVAL, "too many split partials");
   }
 
-  // Workspace layout: items | seqs | tickets | partial (m, l) | partial acc.
+  // Workspace layout: items | seqs | segments | segment ranges | tickets |
+  // partial (m, l) | partial acc.
   size_t o = 0;
   p->off_items = o; o = align256(o + p->items.size() * sizeof(WorkItem));
   p->off_seqs = o; o = align256(o + p->seqs.size() * sizeof(SeqInfo));
+  p->off_segs = o; o = align256(o + p->segs.size() * sizeof(DecodeSeg));
+  p->off_segptr = o; o = align256(o + p->seg_ptr.size() * sizeof(int32_t));
   p->off_ctr = o; o = align256(o + (size_t)num_seqs * num_kv_heads * sizeof(int32_t));
   p->off_ml = o; o = align256(o + (size_t)p->n_partials * 16 * 2 * sizeof(float));
   p->off_part = o; o = align256(o + (size_t)p->n_partials * 16 * head_dim * sizeof(float));
@@ -339,6 +460,9 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
     std::memset(p->pinned, 0, stage);
     if (!p->items.empty()) std::memcpy((char*)p->pinned + p->off_items, p->items.data(), p->items.size() * sizeof(WorkItem));
     if (!p->seqs.empty()) std::memcpy((char*)p->pinned + p->off_seqs, p->seqs.data(), p->seqs.size() * sizeof(SeqInfo));
+    if (!p->segs.empty()) std::memcpy((char*)p->pinned + p->off_segs, p->segs.data(), p->segs.size() * sizeof(DecodeSeg));
+    if (!p->seg_ptr.empty())
+      std::memcpy((char*)p->pinned + p->off_segptr, p->seg_ptr.data(), p->seg_ptr.size() * sizeof(int32_t));
   }
   *out = p;
   return ok();
@@ -348,9 +472,11 @@ size_t gllm_attn_plan_workspace_bytes(const gllm_attn_plan* p) { return p ? p->w
 
 int gllm_attn_plan_info(const gllm_attn_plan* p, int64_t* info, int32_t n) {
   if (!p || !info) return fail(GLLM_ATTN_EINVAL, "null plan or info");
-  const int64_t v[9] = {(int64_t)p->items.size(), p->split_len, p->n_decode_seqs, p->n_prefill_seqs,
-                        p->n_partials, p->total_rows, p->heads_per_wg, p->decode_waves, p->prefill_waves};
-  for (int i = 0; i < n && i < 9; ++i) info[i] = v[i];
+  const int64_t n_wg = p->segs.empty() ? (int64_t)p->items.size() : (int64_t)p->seg_ptr.size() - 1;
+  const int64_t v[10] = {n_wg, p->split_len, p->n_decode_seqs, p->n_prefill_seqs, p->n_partials,
+                         p->total_rows, p->heads_per_wg, p->decode_waves, p->prefill_waves,
+                         (int64_t)p->segs.size()};
+  for (int i = 0; i < n && i < 10; ++i) info[i] = v[i];
   return ok();
 }
 
@@ -433,6 +559,12 @@ int gllm_paged_attention(const gllm_attn_plan* p, const void* q, int64_t q_row_s
   a.seqs = (const SeqInfo*)(p->ws + p->off_seqs);
   a.items = (const WorkItem*)(p->ws + p->off_items);
   a.n_items = (int32_t)p->items.size();
+  if (!p->segs.empty()) {
+    a.segs = (const DecodeSeg*)(p->ws + p->off_segs);
+    a.seg_ptr = (const int32_t*)(p->ws + p->off_segptr);
+    a.n_segs = (int32_t)p->segs.size();
+    a.n_items = (int32_t)p->seg_ptr.size() - 1;
+  }
   a.num_seqs = p->num_seqs;
   a.counters = (int32_t*)(p->ws + p->off_ctr);
   a.partial_ml = (float*)(p->ws + p->off_ml);

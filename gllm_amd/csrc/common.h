@@ -180,4 +180,23 @@ struct WorkItem {
   int32_t partial_base;
 };
 
+// Key range [k0, k1) of one (sequence, kv-head group) for the page-balanced
+// decode launch: the workgroups split the batch's 16-key units evenly, so a
+// sequence's keys may be spread over several workgroups.  Its nseg segments
+// write partials at pbase + head_in_group * nseg + ord; the workgroup that
+// draws the last ticket of counters[ticket] merges them.
+struct DecodeSeg {
+  int32_t seq;
+  int32_t hg;            // kv-head group (heads hg * HW .. hg * HW + HW - 1)
+  int32_t k0, k1;
+  int32_t q_row_start;
+  int32_t ctx_len;
+  int32_t q_len;
+  int32_t nseg;          // segments of this (sequence, group); 1 = written directly
+  int32_t pbase;
+  int32_t ord;
+  int32_t ticket;        // counter index of this (sequence, group)
+  int32_t pad;
+};
+
 }  // namespace gllm

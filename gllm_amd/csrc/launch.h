@@ -69,6 +69,10 @@ struct AttnArgs {
   float* partials;            // [n_partials][16][D] fp32
   float* partial_ml;          // [n_partials][16][2] fp32 (running max in log2 units, sum)
   int32_t* counters;          // [num_seqs * Hkv] split tickets, zero between launches
+  // page-balanced decode (n_segs > 0): workgroup w runs segs[seg_ptr[w] .. seg_ptr[w + 1])
+  const DecodeSeg* segs;
+  const int32_t* seg_ptr;
+  int32_t n_segs;
   int32_t split_len;
   int32_t heads_per_wg;       // decode: kv heads per workgroup (1, 2, 4, 8)
   int32_t decode_waves;       // decode: waves per workgroup (8)

@@ -90,8 +90,19 @@ template <> struct KVChunk<true> {
   __device__ static u32x4 bf16(T x) { return fp8x8_to_bf16x8(x[0], x[1]); }
 };
 
+// One decode task: keys [kbeg, kend) of one sequence for HW kv heads.
+struct DecodeTask {
+  int seq, hg, kbeg, kend, q_row_start, ctx_len, q_len;
+  int nseg;     // tasks of this (sequence, head group); 1: normalise and write the output
+  int pbase;    // partial of head i of the group: pbase + i * nseg + ord
+  int ord;
+  int ticket;   // >= 0: counter whose last ticket merges the partials here; < 0: merge_splits does
+};
+
+// Runs one task with every wave of the workgroup; returns with the workgroup
+// converged (no early exit), so a workgroup can run several tasks in a row.
 template <int D, int HW, int KW, bool KV8>
-__device__ __forceinline__ void decode_wg(const AttnArgs& a, const WorkItem& it, char* lds) {
+__device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask& tk, char* lds, int* ticket_lds) {
   constexpr int NW = HW * KW;
   constexpr int E = KV8 ? 1 : 2;   // bytes per cached element
   using KC = KVChunk<KV8>;
@@ -100,24 +111,28 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, const WorkItem& it,
   constexpr int ND = D / 16;   // 16-dim output blocks
   constexpr int RB = Cfg::kRowBytes;
   constexpr int PF = Cfg::kPF;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // the thread id through an opaque move: nothing derived from it is hoisted
+  // out of a caller's loop over tasks (which would hold it in registers
+  // across the whole main loop)
+  int tid;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
+  const int wave = tid >> 6, lane = tid & 63;
   const int n = lane & 15, grp = lane >> 4;
   const int hi = wave % HW, ki = wave / HW;
-  const int seq = it.seq, split = it.a;
-  const int kvh = (it.kind_b >> 8) * HW + hi;
+  const int seq = tk.seq;
+  const int kvh = tk.hg * HW + hi;
   const bool head_ok = kvh < a.num_kv_heads;
   const int G = a.num_q_heads / a.num_kv_heads;
-  const int R = it.q_len * G;
-  const int L = it.ctx_len + it.q_len;
-  const int kbeg = split * a.split_len;
-  const int kend = min(L, kbeg + a.split_len);
+  const int R = tk.q_len * G;
+  const int kbeg = tk.kbeg;
+  const int kend = tk.kend;
   const int nsub = (kend - kbeg + 15) >> 4;
   const bool row_ok = n < R && head_ok;
   const int r = row_ok ? n / G : 0;
   const int g = row_ok ? n - (n / G) * G : 0;
-  const int64_t qrow = it.q_row_start + r;
+  const int64_t qrow = tk.q_row_start + r;
   const int qh = (head_ok ? kvh : 0) * G + g;
-  const int vis = it.ctx_len + r;
+  const int vis = tk.ctx_len + r;
 
   // Block ids of this split -> LDS (one HBM round trip, off the per-step path).
   int32_t* lbid = reinterpret_cast<int32_t*>(lds + NW * Cfg::kVBytes);
@@ -196,7 +211,7 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, const WorkItem& it,
     float p[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) p[j] = s[j] * sl2;
-    if (kb + 16 > kend || kb + 15 > it.ctx_len) {
+    if (kb + 16 > kend || kb + 15 > tk.ctx_len) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int key = kb + 4 * grp + j;
@@ -251,6 +266,7 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, const WorkItem& it,
   }
   float lt = sum_xor32(sum_xor16(lsum));
 
+  bool lead = true;   // this wave holds its head's state for the task
   if (KW > 1) {
     // merge the KW waves of each head through LDS (reuses the staging area)
     __syncthreads();
@@ -264,42 +280,145 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, const WorkItem& it,
       mml[(wave * 16 + n) * 2 + 1] = lt;
     }
     __syncthreads();
-    if (ki != 0) return;
-    float M = kNegInf;
+    lead = ki == 0;
+    if (lead) {
+      float M = kNegInf;
 #pragma unroll
-    for (int k = 0; k < KW; ++k) M = fmaxf(M, mml[((k * HW + hi) * 16 + n) * 2]);
-    const float Mu = M == kNegInf ? 0.f : M;
-    lt = 0.f;
+      for (int k = 0; k < KW; ++k) M = fmaxf(M, mml[((k * HW + hi) * 16 + n) * 2]);
+      const float Mu = M == kNegInf ? 0.f : M;
+      lt = 0.f;
 #pragma unroll
-    for (int d = 0; d < ND; ++d) acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int d = 0; d < ND; ++d) acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k = 0; k < KW; ++k) {
-      const int w = k * HW + hi;
-      const float wt = fast_exp2(mml[(w * 16 + n) * 2] - Mu);
-      lt += wt * mml[(w * 16 + n) * 2 + 1];
+      for (int k = 0; k < KW; ++k) {
+        const int w = k * HW + hi;
+        const float wt = fast_exp2(mml[(w * 16 + n) * 2] - Mu);
+        lt += wt * mml[(w * 16 + n) * 2 + 1];
 #pragma unroll
-      for (int d = 0; d < ND; ++d) acc[d] += wt * *reinterpret_cast<const f32x4*>(macc + (w * 16 + n) * D + 16 * d + 4 * grp);
+        for (int d = 0; d < ND; ++d)
+          acc[d] += wt * *reinterpret_cast<const f32x4*>(macc + (w * 16 + n) * D + 16 * d + 4 * grp);
+      }
+      m = M;
     }
-    m = M;
   }
-  if (!row_ok) return;
-  if (it.nsplits == 1) {
-    const float inv = 1.f / lt;
-    __bf16* op = (__bf16*)a.out + qrow * a.out_row_stride + (int64_t)qh * D + 4 * grp;
+  const bool wr = lead && row_ok;
+  if (tk.nseg == 1) {
+    if (wr) {
+      __bf16* op = (__bf16*)a.out + qrow * a.out_row_stride + (int64_t)qh * D + 4 * grp;
+      const float inv = 1.f / lt;
 #pragma unroll
-    for (int d = 0; d < ND; ++d)
-      st8(op + 16 * d, u32x2{pack_bf16x2(acc[d][0] * inv, acc[d][1] * inv), pack_bf16x2(acc[d][2] * inv, acc[d][3] * inv)});
+      for (int d = 0; d < ND; ++d)
+        st8(op + 16 * d, u32x2{pack_bf16x2(acc[d][0] * inv, acc[d][1] * inv), pack_bf16x2(acc[d][2] * inv, acc[d][3] * inv)});
+    }
     return;
   }
-  // split partial: unnormalised acc, running max (log2 units) and sum
-  const int64_t pidx = (int64_t)it.partial_base + (int64_t)kvh * it.nsplits + split;
-  float* pa = a.partials + (pidx * 16 + n) * D + 4 * grp;
+  // partial: unnormalised acc, running max (log2 units) and sum
+  const int64_t pfirst = (int64_t)tk.pbase + (int64_t)hi * tk.nseg;
+  if (wr) {
+    float* pa = a.partials + ((pfirst + tk.ord) * 16 + n) * D + 4 * grp;
 #pragma unroll
-  for (int d = 0; d < ND; ++d) *reinterpret_cast<f32x4*>(pa + 16 * d) = acc[d];
-  if (grp == 0) {
-    a.partial_ml[(pidx * 16 + n) * 2] = m;
-    a.partial_ml[(pidx * 16 + n) * 2 + 1] = lt;
+    for (int d = 0; d < ND; ++d) *reinterpret_cast<f32x4*>(pa + 16 * d) = acc[d];
+    if (grp == 0) {
+      a.partial_ml[((pfirst + tk.ord) * 16 + n) * 2] = m;
+      a.partial_ml[((pfirst + tk.ord) * 16 + n) * 2 + 1] = lt;
+    }
   }
+  if (tk.ticket < 0) return;
+  // Ticket: the workgroup that completes a (sequence, group) last merges its
+  // partials.  The barrier orders every wave's partial stores before thread
+  // 0's agent-scope release (L2 write-back, so workgroups on other XCDs see
+  // them); the last ticket holder acquires (L2 invalidate) before reading.
+  // Nobody waits on anybody: a workgroup that is not last simply moves on.
+  __syncthreads();
+  if (tid == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const int t = __hip_atomic_fetch_add(a.counters + tk.ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t == tk.nseg - 1) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      // every ticket of this launch is drawn: re-arm the counter for the next one
+      __hip_atomic_store(a.counters + tk.ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    *ticket_lds = t;
+  }
+  __syncthreads();
+  const bool last = *ticket_lds == tk.nseg - 1;
+  if (!last || !lead || !head_ok) return;
+  // LSE merge, latency-bound (it is the launch's tail): the 16 row lanes of
+  // each 16-lane group are (row mr, partial slot ps) pairs, R rows x PS
+  // slots, and slot ps takes partials ps, ps + PS, ..., CH of them per
+  // round trip with all their loads in flight; the slots are then combined
+  // through shuffles in slot order.  The sums depend only on the partials,
+  // not on which workgroup merges.
+  constexpr int CH = 2;
+  const int PS = 16 / R;
+  const int mr = n % R, ps = n / R;
+  const bool mact = ps < PS;
+  float Mx = kNegInf, Lx = 0.f;
+  f32x4 ox[ND];
+#pragma unroll
+  for (int d = 0; d < ND; ++d) ox[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto combine = [&](float m2, float l2, const f32x4 (&o2)[ND]) {
+    const float nM = fmaxf(Mx, m2);
+    if (nM == kNegInf) return;
+    const float w1 = fast_exp2(Mx - nM), w2 = fast_exp2(m2 - nM);
+    Lx = Lx * w1 + l2 * w2;
+#pragma unroll
+    for (int d = 0; d < ND; ++d) ox[d] = ox[d] * w1 + o2[d] * w2;
+    Mx = nM;
+  };
+  for (int o0 = 0; o0 < tk.nseg; o0 += PS * CH) {
+    float mm[CH], ll[CH];
+    f32x4 vv[CH][ND];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int o = o0 + c * PS + ps;
+      const bool v = mact && o < tk.nseg;
+      const int64_t pi = (pfirst + (v ? o : 0)) * 16 + mr;
+      mm[c] = v ? a.partial_ml[pi * 2] : kNegInf;
+      ll[c] = v ? a.partial_ml[pi * 2 + 1] : 0.f;
+      const float* pa = a.partials + pi * D + 4 * grp;
+#pragma unroll
+      for (int d = 0; d < ND; ++d) vv[c][d] = v ? *reinterpret_cast<const f32x4*>(pa + 16 * d) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c) combine(mm[c], ll[c], vv[c]);
+  }
+  // slot k's state moves to slot 0 (lanes mr + R k -> mr, same 16-dim group)
+  for (int k = 1; k < PS; ++k) {
+    const int src = (lane & 48) | min(15, mr + R * k);
+    const float m2 = __shfl(Mx, src, 64), l2 = __shfl(Lx, src, 64);
+    f32x4 o2[ND];
+#pragma unroll
+    for (int d = 0; d < ND; ++d)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o2[d][j] = __shfl(ox[d][j], src, 64);
+    if (ps == 0) combine(m2, l2, o2);
+  }
+  if (!row_ok) return;   // ps == 0 lanes: mr == n
+  const float inv = 1.f / Lx;
+  __bf16* op = (__bf16*)a.out + qrow * a.out_row_stride + (int64_t)qh * D + 4 * grp;
+#pragma unroll
+  for (int d = 0; d < ND; ++d)
+    st8(op + 16 * d, u32x2{pack_bf16x2(ox[d][0] * inv, ox[d][1] * inv), pack_bf16x2(ox[d][2] * inv, ox[d][3] * inv)});
+}
+
+// One decode work item of the split-launch planner (fixed split_len; split
+// partials merged by merge_splits_kernel).
+template <int D, int HW, int KW, bool KV8>
+__device__ __forceinline__ void decode_wg(const AttnArgs& a, const WorkItem& it, char* lds) {
+  DecodeTask tk;
+  tk.seq = it.seq;
+  tk.hg = it.kind_b >> 8;
+  tk.kbeg = it.a * a.split_len;
+  tk.kend = min(it.ctx_len + it.q_len, tk.kbeg + a.split_len);
+  tk.q_row_start = it.q_row_start;
+  tk.ctx_len = it.ctx_len;
+  tk.q_len = it.q_len;
+  tk.nseg = it.nsplits;
+  tk.pbase = it.partial_base + tk.hg * HW * it.nsplits;
+  tk.ord = it.a;
+  tk.ticket = -1;
+  decode_task<D, HW, KW, KV8>(a, tk, lds, nullptr);
 }
 
 // Combines the split partials of every (sequence, kv head) whose sequence
@@ -822,6 +941,23 @@ __global__ void __launch_bounds__(64 * HW * KW) paged_attn_bf16_kernel(AttnArgs 
   if constexpr (DC) decode_wg<D, HW, KW, KV8>(a, it, lds);
 }
 
+// Page-balanced decode: workgroup w runs its key segments in order (all
+// waves converge between segments; the LDS staging is reused).
+template <int D, int HW, int KW, bool KV8>
+__global__ void __launch_bounds__(64 * HW * KW) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4 : 2)))
+decode_balanced_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) char lds[DecodeCfg<D, HW * KW>::kLdsBytes];
+  __shared__ int ticket;
+  const int s0 = a.seg_ptr[blockIdx.x], s1 = a.seg_ptr[blockIdx.x + 1];
+  for (int s = s0; s < s1; ++s) {
+    if (s > s0) __syncthreads();
+    const DecodeSeg sg = a.segs[s];
+    const DecodeTask tk{sg.seq, sg.hg, sg.k0, sg.k1, sg.q_row_start, sg.ctx_len, sg.q_len,
+                        sg.nseg, sg.pbase, sg.ord, sg.ticket};
+    decode_task<D, HW, KW, KV8>(a, tk, lds, &ticket);
+  }
+}
+
 // Prefill items only.
 template <int D, bool KV8>
 __global__ void __launch_bounds__(64 * kWaves) prefill_bf16_kernel(AttnArgs a) {
@@ -855,8 +991,25 @@ static void launch_paged_hk(const AttnArgs& a, bool pf, bool dc, hipStream_t st)
 }
 
 template <int D, bool KV8>
+static hipError_t launch_decode_balanced(const AttnArgs& a, hipStream_t st) {
+  const dim3 grid(a.n_items);
+  switch (a.heads_per_wg) {
+    case 1: hipLaunchKernelGGL((decode_balanced_kernel<D, 1, 8, KV8>), grid, dim3(512), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((decode_balanced_kernel<D, 2, 4, KV8>), grid, dim3(512), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((decode_balanced_kernel<D, 4, 2, KV8>), grid, dim3(512), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((decode_balanced_kernel<D, 8, 1, KV8>), grid, dim3(512), 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int D, bool KV8>
 static hipError_t launch_paged_d(const AttnArgs& a, bool pf, bool dc, hipStream_t st) {
   const int hw = a.heads_per_wg, nw = a.decode_waves;
+  if (a.n_segs > 0) {
+    if (pf || nw != kWaves) return hipErrorInvalidValue;
+    return launch_decode_balanced<D, KV8>(a, st);
+  }
   if (pf && (a.prefill_waves != kWaves || (dc && nw != kWaves))) return hipErrorInvalidValue;
   if (nw == 8) {
     switch (hw) {

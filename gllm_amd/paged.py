@@ -147,12 +147,18 @@ def build_metadata(block_table: torch.Tensor, seq_lens: torch.Tensor, query_lens
     return slots, pos, cu
 
 
+# split_tokens value that asks for a page-balanced decode plan
+BALANCED = -1
+
+
 class AttentionPlan:
     """Work plan for one batch (built once per engine step, reused by every
     layer).  Lengths are host ints, as ``gllm/llm/llm.py:233-241`` has them.
 
     ``q_seq_stride`` > 0: sequence i's rows start at ``i * q_seq_stride`` (the
-    reference's padded ``[B, T_q]`` layout); 0: packed rows.
+    reference's padded ``[B, T_q]`` layout); 0: packed rows.  ``split_tokens``:
+    0 lets the planner choose, a multiple of 32 fixes the decode split length,
+    ``BALANCED`` deals a decode-only batch's keys evenly to the workgroups.
     """
 
     def __init__(self, query_lens, seq_lens, *, num_q_heads: int, num_kv_heads: int, head_dim: int,
@@ -179,10 +185,10 @@ class AttentionPlan:
         self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         _lib.check(lib.gllm_attn_plan_upload(self._h, self.workspace.data_ptr(), nbytes,
                                              _lib.stream_ptr(self.device)))
-        arr = (ctypes.c_int64 * 9)()
-        _lib.check(lib.gllm_attn_plan_info(self._h, arr, 9))
+        arr = (ctypes.c_int64 * 10)()
+        _lib.check(lib.gllm_attn_plan_info(self._h, arr, 10))
         keys = ("work_items", "split_tokens", "decode_seqs", "prefill_seqs", "partials", "rows", "heads_per_wg",
-                "decode_waves", "prefill_waves")
+                "decode_waves", "prefill_waves", "decode_segments")
         self._info = dict(zip(keys, list(arr)))
         # facts every launch checks, computed once (a plan serves every layer of a step)
         self.rows = self._info["rows"]

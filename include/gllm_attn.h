@@ -55,6 +55,9 @@ enum {
   GLLM_ROPE_BY_ROW = 2       /* cos/sin row = query row index (model.py:195-196 gathered cos_pos) */
 };
 
+/* split_tokens value of gllm_attn_plan_create: page-balanced decode plan */
+enum { GLLM_SPLIT_BALANCED = -1 };
+
 typedef struct gllm_attn_plan gllm_attn_plan;
 
 /* Thread-local message of the last failing call ("" if none). */
@@ -112,7 +115,12 @@ int gllm_rope_kv_write(const void* q, void* q_out, const void* k, const void* v,
  * context + query length, as llm.py:233-236.  split_tokens = context tokens
  * per decode split (multiple of 32) and decode_heads_per_wg = kv heads one
  * decode workgroup serves (1, 2, 4 or 8); 0 lets the planner choose both from
- * the batch and the CU count.  No device work happens here.
+ * the batch and the CU count.  split_tokens == GLLM_SPLIT_BALANCED (-1) plans
+ * a decode-only batch page-balanced: its keys (16-key units per sequence and
+ * kv-head group) are dealt out evenly to one workgroup per resident CU slot,
+ * and sequences spread over several workgroups are merged inside the same
+ * launch (split tickets); 0 picks it for decode-only batches whose workgroups
+ * would each stream >= 2048 keys.  No device work happens here.
  */
 int gllm_attn_plan_create(gllm_attn_plan** plan, const int32_t* query_lens,
                           const int32_t* seq_lens, int32_t num_seqs, int64_t q_seq_stride,
@@ -127,7 +135,8 @@ int gllm_attn_plan_upload(gllm_attn_plan* plan, void* workspace, size_t workspac
 /* Plan facts: [0] work items, [1] split length, [2] decode-path sequences,
  * [3] prefill-path sequences, [4] split partials, [5] total query rows,
  * [6] kv heads per decode workgroup, [7] waves per decode workgroup,
- * [8] waves per prefill workgroup. */
+ * [8] waves per prefill workgroup, [9] page-balanced decode segments (0:
+ * split planner).  [0] counts workgroups for a page-balanced plan. */
 int gllm_attn_plan_info(const gllm_attn_plan* plan, int64_t* info, int32_t n);
 int gllm_attn_plan_destroy(gllm_attn_plan* plan);
 

@@ -56,6 +56,48 @@ def test_planner_host_logic():
     assert lib.gllm_attn_plan_destroy(h) == 0
 
 
+def _plan_info(lib, ql, sl, hq, hkv, d, split=0, hw=0):
+    h = ctypes.c_void_p()
+    n = len(ql)
+    rc = lib.gllm_attn_plan_create(ctypes.byref(h), (ctypes.c_int32 * n)(*ql), (ctypes.c_int32 * n)(*sl), n, 0,
+                                   hq, hkv, d, 16, _lib.DTYPE_BF16, split, hw)
+    if rc:
+        return rc, None
+    info = (ctypes.c_int64 * 10)()
+    assert lib.gllm_attn_plan_info(h, info, 10) == 0
+    assert lib.gllm_attn_plan_destroy(h) == 0
+    return 0, dict(zip(("wgs", "split", "ndec", "npf", "parts", "rows", "hw", "dw", "pw", "segs"), list(info)))
+
+
+def test_planner_page_balanced():
+    """Page-balanced decode plans (GLLM_SPLIT_BALANCED = -1, or chosen for
+    long-context batches): 16-key units per (sequence, kv-head group) dealt
+    to min(units, resident slots) workgroups (256 CUs off-GPU: 512 at D = 64,
+    256 at D = 128)."""
+    from gllm_amd import workloads
+    lib = _lib.load()
+    # 7 + 125 units <= 512 workgroups: one unit each, every unit its own segment;
+    # partials: 8 heads x segments of each split sequence
+    rc, i = _plan_info(lib, [1, 1], [100, 2000], 32, 8, 64, split=-1)
+    assert rc == 0 and (i["wgs"], i["segs"], i["parts"], i["hw"], i["split"]) == (132, 132, 8 * 132, 8, 0)
+    # Hkv 12 -> 4 heads per workgroup, 3 groups; Hkv 2 -> 2
+    assert _plan_info(lib, [1], [64], 48, 12, 64, split=-1)[1]["hw"] == 4
+    assert _plan_info(lib, [1], [64], 16, 2, 64, split=-1)[1]["hw"] == 2
+    # short contexts (config b) stay on the split planner, long ones (config e) go balanced
+    b, e = workloads.config_b(), workloads.config_e()
+    rc, i = _plan_info(lib, b.q_lens, b.seq_lens, 32, 8, 64)
+    assert rc == 0 and i["segs"] == 0
+    rc, i = _plan_info(lib, b.q_lens, b.seq_lens, 32, 8, 64, split=-1)
+    assert rc == 0 and i["wgs"] == 512 and i["segs"] >= 512
+    rc, i = _plan_info(lib, e.q_lens, e.seq_lens, 64, 8, 128)
+    assert rc == 0 and i["wgs"] == 256 and i["segs"] >= 256 and i["hw"] == 8
+    # a segment caches at most 512 block ids: >= 8192 keys per workgroup means cuts
+    assert i["segs"] >= sum(-(-L // 8192) for L in e.seq_lens)
+    # prefill-path sequences cannot be planned page-balanced
+    rc, _ = _plan_info(lib, [1, 40], [100, 80], 32, 8, 64, split=-1)
+    assert rc == _lib.EINVAL and b"decode-only" in lib.gllm_attn_last_error()
+
+
 @pytest.mark.parametrize("args,code", [
     (dict(ql=[0], sl=[5]), _lib.EINVAL),           # empty query
     (dict(ql=[6], sl=[5]), _lib.EINVAL),           # seq shorter than query
@@ -63,6 +105,7 @@ def test_planner_host_logic():
     (dict(bs=12), _lib.EUNSUPPORTED),              # block size not a power of two
     (dict(d=96), _lib.EUNSUPPORTED),               # bf16 head_dim
     (dict(split=48), _lib.EINVAL),                 # split not a multiple of 32
+    (dict(split=-2), _lib.EINVAL),                 # negative split other than GLLM_SPLIT_BALANCED
     (dict(hw=3), _lib.EINVAL),                     # heads per decode workgroup
 ])
 def test_planner_rejects(args, code):

@@ -29,7 +29,7 @@ def _plan(b, **kw):
 
 
 @pytest.mark.parametrize("Hq,Hkv,D", [(32, 8, 64), (32, 8, 128), (64, 8, 128), (16, 1, 64)])
-@pytest.mark.parametrize("split", [0, 96])
+@pytest.mark.parametrize("split", [0, 96, paged.BALANCED])
 def test_fp8_decode_parity(Hq, Hkv, D, split):
     print(f"fp8 decode Hq={Hq} Hkv={Hkv} D={D} split={split}", flush=True)
     b = _fp8(make_batch([0, 15, 16, 300, 1000, 2047], [1] * 6, Hq, Hkv, D))

@@ -60,7 +60,8 @@ def test_config_b_decode_full():
     b = workloads.materialize(workloads.config_b(), DEV, values_on_device=True)
     ref = _oracle_rows(b, [(i, 0) for i in range(len(b.q_lens))], b.q.cpu())
     outs = []
-    for hw, split in ((0, 0), (1, 0), (2, 0), (4, 0), (8, 0), (2, 256), (8, 128)):
+    B = paged.BALANCED
+    for hw, split in ((0, 0), (1, 0), (2, 0), (4, 0), (8, 0), (2, 256), (8, 128), (0, B), (2, B), (4, B), (1, B)):
         out = paged.paged_attention(_plan(b, heads_per_wg=hw, split_tokens=split), b.q, b.k_cache, b.v_cache,
                                     b.block_table)
         torch.cuda.synchronize()
@@ -117,6 +118,7 @@ def test_config_e_long_decode():
     print("config e full", flush=True)
     b = workloads.materialize(workloads.config_e(), DEV, values_on_device=True)
     out = paged.paged_attention(_plan(b), b.q, b.k_cache, b.v_cache, b.block_table)
+    assert _plan(b).info["decode_segments"] > 0       # long contexts: page-balanced plan
     out2 = paged.paged_attention(_plan(b, heads_per_wg=8, split_tokens=2048), b.q, b.k_cache, b.v_cache,
                                  b.block_table)
     torch.cuda.synchronize()

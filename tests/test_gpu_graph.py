@@ -17,6 +17,8 @@ CASES = {
     "decode": dict(ctx=[300, 17, 1500, 64, 900], ql=[1] * 5, Hq=32, Hkv=8, D=64, split=0),
     # decode with context splits (merge_splits_kernel runs in the graph too)
     "decode_split": dict(ctx=[4000, 33, 2500], ql=[1] * 3, Hq=64, Hkv=8, D=128, split=512),
+    # page-balanced decode: split tickets drawn and re-armed inside the graph
+    "decode_balanced": dict(ctx=[4000, 33, 2500, 700, 90], ql=[1] * 5, Hq=32, Hkv=8, D=64, split=paged.BALANCED),
     # mixed continuous batch: decodes plus two prefill chunks
     "mixed": dict(ctx=[700, 0, 250, 40], ql=[1, 90, 1, 33], Hq=32, Hkv=8, D=128, split=0),
 }

@@ -95,7 +95,7 @@ def test_fp8_cache_cast_exhaustive():
 
 # ------------------------------------------------------------ (b) decode
 @pytest.mark.parametrize("Hq,Hkv,D", [(32, 8, 64), (32, 8, 128), (64, 8, 128), (8, 8, 64), (16, 1, 64)])
-@pytest.mark.parametrize("split", [0, 32, 96])
+@pytest.mark.parametrize("split", [0, 32, 96, paged.BALANCED])
 def test_decode_parity(Hq, Hkv, D, split):
     print(f"decode Hq={Hq} Hkv={Hkv} D={D} split={split}", flush=True)
     lens = [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 100, 255, 256, 257, 700, 1025]
@@ -109,15 +109,40 @@ def test_decode_parity(Hq, Hkv, D, split):
         assert_close_bf16(out, ref, f"decode rep {rep}")
 
 
-def test_decode_multi_query_rows():
-    """q_len * G <= 16 stays on the decode path with a causal mask inside it."""
-    print("decode multi-query", flush=True)
-    b = make_batch([40, 0, 200, 7], [4, 3, 2, 4], 16, 4, 64)
+@pytest.mark.parametrize("split", [0, 64, paged.BALANCED])
+def test_decode_multi_query_rows(split):
+    """q_len * G <= 16 stays on the decode path with a causal mask inside it
+    (page-balanced: a segment past a row's last visible key leaves that row's
+    partial empty)."""
+    print(f"decode multi-query split={split}", flush=True)
+    b = make_batch([40, 0, 200, 7, 1000], [4, 3, 2, 4, 4], 16, 4, 64)
     plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=16, num_kv_heads=4, head_dim=64,
-                               block_size=16, dtype=torch.bfloat16, device=DEV, split_tokens=64)
-    assert plan.info["decode_seqs"] == 4
-    out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
-    assert_close_bf16(out, oracle_paged(b), "decode multi-row")
+                               block_size=16, dtype=torch.bfloat16, device=DEV, split_tokens=split)
+    assert plan.info["decode_seqs"] == 5
+    for rep in range(2):
+        out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
+        torch.cuda.synchronize()
+        assert_close_bf16(out, oracle_paged(b), f"decode multi-row rep {rep}")
+
+
+@pytest.mark.parametrize("bs", [4, 8, 32, 64])
+@pytest.mark.parametrize("Hq,Hkv,D", [(16, 2, 64), (32, 4, 128), (48, 12, 64)])
+def test_decode_balanced_shapes(bs, Hq, Hkv, D):
+    """Page-balanced decode over block sizes (segment cuts at 16-key units,
+    not block boundaries) and kv-head groupings (Hkv 2 / 4 -> 2 / 4 heads
+    per workgroup, Hkv 12 -> three groups of 4)."""
+    print(f"decode balanced bs={bs} Hq={Hq} Hkv={Hkv} D={D}", flush=True)
+    lens = [1, 9, 16, 47, 130, 511, 2100, 3000]
+    b = make_batch([L - 1 for L in lens], [1] * len(lens), Hq, Hkv, D, bs=bs)
+    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D,
+                               block_size=bs, dtype=torch.bfloat16, device=DEV, split_tokens=paged.BALANCED)
+    info = plan.info
+    assert info["decode_segments"] > 0 and info["heads_per_wg"] == (2 if Hkv == 2 else 4)
+    ref = oracle_paged(b)
+    for rep in range(2):
+        out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
+        torch.cuda.synchronize()
+        assert_close_bf16(out, ref, f"balanced rep {rep}")
 
 
 # ------------------------------------------------------------ (c) prefill
