@@ -134,32 +134,45 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
   const int qh = (head_ok ? kvh : 0) * G + g;
   const int vis = tk.ctx_len + r;
 
-  // Block ids of this split -> LDS (one HBM round trip, off the per-step path).
+  // Prologue: the block ids of this task (-> LDS), the Q rows and their
+  // cos/sin rows are loaded together, one HBM round trip before the first
+  // K/V loads can be addressed (the block-id load is issued first so its LDS
+  // store does not wait for the others).
+  static_assert(Cfg::kMaxBlocks <= 64 * NW, "one block id per thread");
   int32_t* lbid = reinterpret_cast<int32_t*>(lds + NW * Cfg::kVBytes);
   const int blk0 = kbeg >> a.block_shift;
   const int nblk = ((kend - 1) >> a.block_shift) - blk0 + 1;
   const int32_t* bt = a.block_table + (int64_t)seq * a.block_table_stride + blk0;
-  for (int i = tid; i < nblk; i += 64 * NW) {
-    const uint32_t b = (uint32_t)bt[i];
-    lbid[i] = b < (uint64_t)a.num_blocks ? (int32_t)b : 0;  // never address outside the pool
+  const uint32_t bid = tid < nblk ? (uint32_t)bt[tid] : 0u;
+  const __bf16* qp = (const __bf16*)a.q + qrow * a.q_row_stride + (int64_t)qh * D + 8 * grp;
+  u32x4 qraw[NK], craw[NK / 2], sraw[NK / 2];
+#pragma unroll
+  for (int kk = 0; kk < NK; ++kk) qraw[kk] = ld16(qp + 32 * kk);
+  const bool rope = a.rope_mode != kRopeNone;
+  if (rope) {
+    const int64_t crow = a.rope_mode == kRopeByPosition ? (int64_t)vis : qrow;
+    const __bf16* cp = (const __bf16*)a.rope_cos + crow * a.rope_row_stride + 8 * grp;
+    const __bf16* sp = (const __bf16*)a.rope_sin + crow * a.rope_row_stride + 8 * grp;
+#pragma unroll
+    for (int kk = 0; kk < NK / 2; ++kk) {
+      craw[kk] = ld16(cp + 32 * kk);
+      sraw[kk] = ld16(sp + 32 * kk);
+    }
   }
+  if (tid < nblk) lbid[tid] = bid < (uint64_t)a.num_blocks ? (int32_t)bid : 0;  // never address outside the pool
 
   // Q as the B operand of S^T = K Q^T: lane holds Q[row n][32kk + 8grp + i].
   bf16x8 qB[NK];
   {
-    const __bf16* qp = (const __bf16*)a.q + qrow * a.q_row_stride + (int64_t)qh * D + 8 * grp;
     float x[NK][8];
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) unpack_bf16x8(ld16(qp + 32 * kk), x[kk]);
-    if (a.rope_mode != kRopeNone) {
-      const int64_t crow = a.rope_mode == kRopeByPosition ? (int64_t)vis : qrow;
-      const __bf16* cp = (const __bf16*)a.rope_cos + crow * a.rope_row_stride + 8 * grp;
-      const __bf16* sp = (const __bf16*)a.rope_sin + crow * a.rope_row_stride + 8 * grp;
+    for (int kk = 0; kk < NK; ++kk) unpack_bf16x8(qraw[kk], x[kk]);
+    if (rope) {
 #pragma unroll
       for (int kk = 0; kk < NK / 2; ++kk) {
         float c[8], s[8];
-        unpack_bf16x8(ld16(cp + 32 * kk), c);
-        unpack_bf16x8(ld16(sp + 32 * kk), s);
+        unpack_bf16x8(craw[kk], c);
+        unpack_bf16x8(sraw[kk], s);
         rope8_bf16(x[kk], x[kk + NK / 2], c, s);
       }
     }
@@ -189,7 +202,9 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
   const int ntw = head_ok && nsub > ki ? (nsub - ki + KW - 1) / KW : 0;
   typename KC::T kr[PF + 1][NK], vr[PF + 1][NK];
   auto issue = [&](int t, typename KC::T (&kd)[NK], typename KC::T (&vd)[NK]) {
-    const int key = min(kbeg + 16 * (ki + KW * t) + n, kend - 1);
+    // ring padding (t >= ntw): every lane reads the task's last slot, one
+    // cache line per load instead of a whole 16-key tile
+    const int key = t < ntw ? min(kbeg + 16 * (ki + KW * t) + n, kend - 1) : kend - 1;
     const uint32_t slot = (uint32_t)lbid[(key >> a.block_shift) - blk0] * (uint32_t)a.block_size + ((uint32_t)key & bmask);
     const uint64_t off = (uint64_t)slot * sbytes;
 #pragma unroll
@@ -242,22 +257,22 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
   };
 
   // The ring loop has no early exit and issues loads unconditionally (tiles
-  // past the end re-read the last tile, a cache hit, and are masked), so the
-  // in-flight load order is the same on every path and the PF tiles in
-  // flight really overlap the compute of the current one.  sched_barrier
-  // keeps the scheduler from reordering the issues.
+  // past the end read one cached slot and are masked), so the in-flight load
+  // order is the same on every path and the compiler's waits keep PF tiles
+  // in flight while the current one is computed (conditional issues would
+  // make it wait for all of them).  sched_barrier keeps the scheduler from
+  // reordering the issues.
   if (ntw > 0) {
-    const int tlast = ntw - 1;
 #pragma unroll
     for (int u = 0; u < PF; ++u) {
-      issue(min(u, tlast), kr[u], vr[u]);
+      issue(u, kr[u], vr[u]);
       __builtin_amdgcn_sched_barrier(0);
     }
     for (int t0 = 0; t0 < ntw; t0 += PF + 1) {
 #pragma unroll
       for (int u = 0; u <= PF; ++u) {
         const int t = t0 + u;
-        issue(min(t + PF, tlast), kr[(u + PF) % (PF + 1)], vr[(u + PF) % (PF + 1)]);
+        issue(t + PF, kr[(u + PF) % (PF + 1)], vr[(u + PF) % (PF + 1)]);
         __builtin_amdgcn_sched_barrier(0);
         compute(t, kr[u], vr[u]);
         __builtin_amdgcn_sched_barrier(0);
