@@ -256,19 +256,20 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
     for (int d = 0; d < ND; ++d) acc[d] = mfma16k16(lds_read_tr16(vrow + 32 * d), pb, acc[d]);
   };
 
-  // The ring loop has no early exit and issues loads unconditionally (tiles
-  // past the end read one cached slot and are masked), so the in-flight load
-  // order is the same on every path and the compiler's waits keep PF tiles
-  // in flight while the current one is computed (conditional issues would
-  // make it wait for all of them).  sched_barrier keeps the scheduler from
-  // reordering the issues.
+  // The ring issues loads unconditionally (tiles past the end read one
+  // cached slot and are masked), so the in-flight load order is the same on
+  // every path and the compiler's waits keep PF tiles in flight while the
+  // current one is computed (conditional issues would make it wait for all
+  // of them); the tail after the last whole group issues nothing.
+  // sched_barrier keeps the scheduler from reordering the issues.
   if (ntw > 0) {
 #pragma unroll
     for (int u = 0; u < PF; ++u) {
       issue(u, kr[u], vr[u]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    for (int t0 = 0; t0 < ntw; t0 += PF + 1) {
+    int t0 = 0;
+    for (; t0 + PF < ntw; t0 += PF + 1) {   // whole groups: all PF + 1 computes are real tiles
 #pragma unroll
       for (int u = 0; u <= PF; ++u) {
         const int t = t0 + u;
@@ -278,6 +279,10 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    // last ntw - t0 (<= PF) tiles: already in flight, nothing more to issue
+#pragma unroll
+    for (int u = 0; u < PF; ++u)
+      if (t0 + u < ntw) compute(t0 + u, kr[u], vr[u]);
   }
   float lt = sum_xor32(sum_xor16(lsum));
 
