@@ -50,7 +50,7 @@ __device__ __forceinline__ int64_t paged_slot(const AttnArgs& a, const int32_t* 
 constexpr int kWaves = 8;   // waves per workgroup (both paths; one block size)
 
 template <int D, int NW> struct DecodeCfg {
-  static constexpr int kPF = D == 64 ? 3 : 2;          // sub-tiles in flight per wave
+  static constexpr int kPF = 2;                         // sub-tiles in flight per wave (2 beat 3 at D = 64)
   static constexpr int kRowBytes = D * 2 + 32;         // V staging row stride (bytes)
   static constexpr int kVBytes = 16 * kRowBytes;       // per-wave V staging: 16 keys
   static constexpr int kMaxBlocks = 512;               // block ids of one split, cached in LDS
