@@ -8,13 +8,14 @@
 // pattern gllm/llm/llm.py:259-274 builds, on every real query row.  GQA: query
 // head h reads kv head h / G (gllm/ops/attention/reference_attention.py:19-30).
 //
-// Decode (one 8-wave workgroup per (sequence, context split, 8 kv heads)):
-//   all waves walk the same keys, one kv head each, so every step streams
-//   whole pages; S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with K loaded from
+// Decode (8-wave workgroups; a task = one key range of one sequence for HW
+//   kv heads): S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with K loaded from
 //   HBM straight into MFMA operand registers (16-byte loads) through a
 //   prefetch ring; online softmax in fp32 (log2 domain, lazy rescale);
 //   O^T += V^T P^T on v_mfma_f32_16x16x16_bf16 with V transposed through LDS
-//   by ds_read_b64_tr_b16; split sequences are merged by a second small launch.
+//   by ds_read_b64_tr_b16.  Split plans merge split partials in a second
+//   small launch; page-balanced plans deal equal key ranges to the
+//   workgroups and merge in the same launch (split tickets).
 // Prefill (one 8-wave workgroup per (sequence, kv head, 8 row tiles of 32)):
 //   K/V tiles of 64 keys staged in LDS, S^T = K Q^T and O^T += V^T P^T on
 //   v_mfma_f32_32x32x16_bf16, flash-style running max/sum, causal tile skip.
