@@ -153,6 +153,50 @@ def bench_prefill(b, copies, warmup, steps, dev):
     }
 
 
+def bench_qkv(n_tokens, hidden, Hq, Hkv, D, weight_copies, warmup, steps, dev, seed=5):
+    """Fused QKV projection + RoPE + KV write (``gllm_qkv_rope_kv_write``) vs
+    the unfused path (three bf16 GEMMs through torch/hipBLASLt + the RoPE/KV
+    write kernel), both graph-timed.  Weight copies are rotated so a decode
+    step's weights come from HBM, not the 256 MB Infinity Cache."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    bf = torch.bfloat16
+    x = torch.randn(n_tokens, hidden, device=dev, generator=g, dtype=torch.float32).to(bf)
+    ws = []
+    for _ in range(weight_copies):
+        w = [(torch.randn(h * D, hidden, device=dev, generator=g) / hidden ** 0.5).to(bf) for h in (Hq, Hkv, Hkv)]
+        ws.append((w, [t.t().contiguous() for t in w]))        # [out, in] and its transpose for torch.mm
+    max_pos = 8192
+    inv = 500000.0 ** (-2 * torch.arange(D // 2, device=dev) / D)
+    ang = torch.arange(max_pos, device=dev).unsqueeze(1) * inv
+    cos, sin = torch.cos(ang).to(bf), torch.sin(ang).to(bf)
+    pos = torch.randint(0, max_pos, (n_tokens,), device=dev, generator=g)
+    ns = n_tokens + 16
+    slots = torch.randperm(ns, device=dev, generator=g)[:n_tokens].contiguous()
+    kc = torch.zeros(ns, Hkv, D, dtype=bf, device=dev)
+    vc = torch.zeros_like(kc)
+    q_out = torch.empty(n_tokens, Hq, D, dtype=bf, device=dev)
+
+    def fused(w):
+        paged.qkv_rope_kv_write(x, w[0], w[1], w[2], cos, sin, kc, vc, slots, q_out=q_out, rope_rows=pos)
+
+    def unfused(wt):
+        q = torch.mm(x, wt[0])
+        k = torch.mm(x, wt[1])
+        v = torch.mm(x, wt[2])
+        paged.rope_kv_write(k.view(n_tokens, Hkv, D), v.view(n_tokens, Hkv, D), cos, sin, kc, vc, slots,
+                            q=q.view(n_tokens, Hq, D), q_out=q_out, rope_rows=pos)
+
+    tf = _graph_time([lambda w=w: fused(w) for w, _ in ws], warmup, steps)
+    tu = _graph_time([lambda wt=wt: unfused(wt) for _, wt in ws], warmup, steps)
+    flops = 2 * n_tokens * (Hq + 2 * Hkv) * D * hidden
+    wbytes = (Hq + 2 * Hkv) * D * hidden * 2
+    iobytes = wbytes + n_tokens * hidden * 2 + n_tokens * (Hq + 2 * Hkv) * D * 2
+    return {"tokens": n_tokens, "hidden": hidden, "fused_ms": tf, "unfused_ms": tu, "speedup": tu / tf,
+            "tflops": flops / (tf * 1e-3) / 1e12, "mfma_frac": flops / (tf * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+            "gbs": iobytes / (tf * 1e-3) / 1e9, "hbm_frac": iobytes / (tf * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "weight_copies": weight_copies}
+
+
 def bench_metadata(b: workloads.PagedBatch, warmup, steps, dev, cpu: bool):
     """Device metadata builder (query-row slots + positions + cu_seqlens) on
     one batch; with ``cpu`` also the reference path's host builder
@@ -255,8 +299,15 @@ def main():
         r8["speedup_vs_bf16_kv"] = head["ms_per_step"] / r8["ms_per_step"]
         extra["decode_1b_fp8kv"] = r8
         torch.cuda.empty_cache()
+        # fused QKV projection + RoPE + KV write for the same 64 decode tokens (1B layer)
+        extra["qkv_decode_1b"] = bench_qkv(64, 2048, 32, 8, 64, 24, args.warmup, args.steps, dev)
+        torch.cuda.empty_cache()
     if "c" in cfgs:
         extra["prefill_8b"] = bench_prefill(workloads.config_c(), 2, args.warmup, args.steps, dev)
+        torch.cuda.empty_cache()
+        # fused QKV projection + RoPE + KV write for config (c)'s tokens (8B layer)
+        extra["qkv_prefill_8b"] = bench_qkv(workloads.config_c().rows, 4096, 32, 8, 128, 2, args.warmup,
+                                            max(5, args.steps // 3), dev)
         torch.cuda.empty_cache()
     if "d" in cfgs:
         r, xd, _ = bench_decode(workloads.config_d(), 1, args.warmup, args.steps, args.split, dev, args.hw)

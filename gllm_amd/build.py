@@ -20,8 +20,9 @@ LIB = os.path.join(LIBDIR, "libgllm_attn.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["api.hip", "rope_kv_write.hip", "paged_attention.hip", "attention_f32.hip", "metadata.hip"]
-NO_CONTRACT = {"rope_kv_write.hip", "attention_f32.hip"}
+SOURCES = ["api.hip", "rope_kv_write.hip", "paged_attention.hip", "attention_f32.hip", "metadata.hip",
+           "qkv_proj.hip"]
+NO_CONTRACT = {"rope_kv_write.hip", "attention_f32.hip", "qkv_proj.hip"}
 # MFMA accumulators stay in VGPRs (no per-tile AGPR<->VGPR copies)
 EXTRA = {"paged_attention.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"]}
 COMMON = [

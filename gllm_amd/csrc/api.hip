@@ -234,6 +234,48 @@ int gllm_rope_kv_write(const void* q, void* q_out, const void* k, const void* v,
   return hip_check(launch_rope_kv_write(a, (hipStream_t)stream), "rope_kv_write launch");
 }
 
+int gllm_qkv_rope_kv_write(const void* x, int64_t x_row_stride, int64_t num_tokens, int32_t hidden,
+                           const void* w_q, int64_t w_q_row_stride, const void* w_k, int64_t w_k_row_stride,
+                           const void* w_v, int64_t w_v_row_stride, void* q_out, int64_t q_out_row_stride,
+                           int32_t rotate_q, void* k_cache, void* v_cache, int64_t cache_slot_stride,
+                           int64_t num_slots, const int64_t* slot_mapping, const int32_t* query_lens,
+                           int64_t tokens_per_seq, const void* cos, const void* sin, const int64_t* rope_rows,
+                           int64_t rope_row_stride, int32_t num_q_heads, int32_t num_kv_heads,
+                           int32_t head_dim, int32_t dtype, int32_t kv_dtype, void* stream) {
+  if (num_tokens < 0) return fail(GLLM_ATTN_EINVAL, "num_tokens < 0");
+  if (dtype != GLLM_DTYPE_BF16) return fail(GLLM_ATTN_EUNSUPPORTED, "fused QKV projection needs a bf16 model (dtype %d)", dtype);
+  if (kv_dtype != GLLM_DTYPE_BF16 && kv_dtype != GLLM_DTYPE_FP8_E4M3)
+    return fail(GLLM_ATTN_EUNSUPPORTED, "kv_dtype %d (bf16 or fp8 e4m3fn)", kv_dtype);
+  if (head_dim != 64 && head_dim != 128) return fail(GLLM_ATTN_EUNSUPPORTED, "head_dim %d (64 or 128)", head_dim);
+  if (num_q_heads <= 0 || num_kv_heads <= 0) return fail(GLLM_ATTN_EINVAL, "head counts must be > 0");
+  if (hidden <= 0 || hidden % 32) return fail(GLLM_ATTN_EUNSUPPORTED, "hidden %d must be a positive multiple of 32", hidden);
+  if (!x || !w_k || !w_v || !k_cache || !v_cache || !slot_mapping || !cos || !sin)
+    return fail(GLLM_ATTN_EINVAL, "null pointer argument");
+  if (q_out && !w_q) return fail(GLLM_ATTN_EINVAL, "q_out given without w_q");
+  auto aligned16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  if (!aligned16(x) || !aligned16(w_k) || !aligned16(w_v) || (q_out && !aligned16(w_q)))
+    return fail(GLLM_ATTN_EINVAL, "x and the weights must be 16-byte aligned");
+  if (x_row_stride < hidden || x_row_stride % 8 || w_k_row_stride < hidden || w_k_row_stride % 8 ||
+      w_v_row_stride < hidden || w_v_row_stride % 8 || (q_out && (w_q_row_stride < hidden || w_q_row_stride % 8)))
+    return fail(GLLM_ATTN_EINVAL, "row strides must be >= hidden and multiples of 8 elements");
+  if (q_out && q_out_row_stride < (int64_t)num_q_heads * head_dim)
+    return fail(GLLM_ATTN_EINVAL, "q_out row stride < num_q_heads * head_dim");
+  if (cache_slot_stride < (int64_t)num_kv_heads * head_dim) return fail(GLLM_ATTN_EINVAL, "cache_slot_stride too small");
+  if (num_slots <= 0) return fail(GLLM_ATTN_EINVAL, "num_slots must be > 0");
+  if (rope_row_stride < head_dim / 2) return fail(GLLM_ATTN_EINVAL, "rope_row_stride < head_dim / 2");
+  if (query_lens && tokens_per_seq <= 0) return fail(GLLM_ATTN_EINVAL, "tokens_per_seq must be > 0 with query_lens");
+  QKVArgs a{};
+  a.x = x; a.x_row_stride = x_row_stride; a.num_tokens = num_tokens; a.hidden = hidden;
+  a.w_q = w_q; a.w_k = w_k; a.w_v = w_v;
+  a.w_q_row_stride = w_q_row_stride; a.w_k_row_stride = w_k_row_stride; a.w_v_row_stride = w_v_row_stride;
+  a.q_out = q_out; a.q_out_row_stride = q_out_row_stride; a.rotate_q = rotate_q ? 1 : 0;
+  a.k_cache = k_cache; a.v_cache = v_cache; a.cache_slot_stride = cache_slot_stride; a.num_slots = num_slots;
+  a.slot_mapping = slot_mapping; a.query_lens = query_lens; a.tokens_per_seq = tokens_per_seq;
+  a.cos = cos; a.sin = sin; a.rope_rows = rope_rows; a.rope_row_stride = rope_row_stride;
+  a.num_q_heads = num_q_heads; a.num_kv_heads = num_kv_heads; a.head_dim = head_dim; a.kv_dtype = kv_dtype;
+  return hip_check(launch_qkv_rope_write(a, (hipStream_t)stream), "qkv projection launch");
+}
+
 int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const int32_t* seq_lens,
                           int32_t num_seqs, int64_t q_seq_stride, int32_t num_q_heads,
                           int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t dtype,

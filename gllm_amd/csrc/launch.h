@@ -97,7 +97,35 @@ struct MetadataArgs {
   int64_t num_rows;
 };
 
+// Fused QKV projection + RoPE + paged KV write (bf16 model).
+struct QKVArgs {
+  const void* x;                 // [num_tokens, x_row_stride] bf16
+  int64_t x_row_stride;
+  int64_t num_tokens;
+  int32_t hidden;                // K of the projection (multiple of 32)
+  const void* w_q;               // [Hq * D, hidden] bf16, row stride w_q_row_stride
+  const void* w_k;               // [Hkv * D, hidden]
+  const void* w_v;               // [Hkv * D, hidden]
+  int64_t w_q_row_stride, w_k_row_stride, w_v_row_stride;
+  void* q_out;                   // nullable: [num_tokens, q_out_row_stride] bf16
+  int64_t q_out_row_stride;
+  int32_t rotate_q;
+  void* k_cache;
+  void* v_cache;
+  int64_t cache_slot_stride, num_slots;
+  const int64_t* slot_mapping;   // [num_tokens]
+  const int32_t* query_lens;     // nullable: skip row r >= query_lens[tok / tokens_per_seq]
+  int64_t tokens_per_seq;
+  const void* cos;               // [rows, rope_row_stride] bf16
+  const void* sin;
+  const int64_t* rope_rows;      // nullable: cos/sin row per token (else the token index)
+  int64_t rope_row_stride;
+  int32_t num_q_heads, num_kv_heads, head_dim;
+  int32_t kv_dtype;
+};
+
 hipError_t launch_rope_kv_write(const RopeKVWriteArgs& a, hipStream_t stream);
+hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t stream);
 hipError_t launch_build_metadata(const MetadataArgs& a, hipStream_t stream);
 hipError_t launch_paged_attention_bf16(const AttnArgs& a, bool has_prefill, bool has_decode, hipStream_t stream);
 hipError_t launch_dense_attention_bf16(const AttnArgs& a, int B, int Tq, hipStream_t stream);

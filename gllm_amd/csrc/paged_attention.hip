@@ -484,20 +484,6 @@ template <int D, int NS> struct PrefillCfg {
   static constexpr int kLdsBytes = kStages * kStage + kBidCache * 4;
 };
 
-// Direct global -> LDS copy of 16 bytes per lane: lane l's bytes land at
-// lds_base + 16 l (lds_base wave-uniform, in M0).  Written as inline asm so
-// the compiler does not wait for every outstanding copy before each LDS read;
-// the kernel waits for its own copies with wait_vmcnt before the barrier that
-// publishes a stage.
-__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_base) : "memory", "m0");
-}
-// s_waitcnt vmcnt(N) leaving the other counters alone (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
 
 // Logical 16-byte chunk c of LDS row r is stored at chunk c ^ pf_swz(r).  The
 // pattern keeps the three access shapes of a tile free of bank conflicts:

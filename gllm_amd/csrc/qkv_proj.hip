@@ -1,0 +1,249 @@
+// Fused QKV projection + RoPE + paged KV write for gfx950: replaces
+// gllm/model/layers/attention.py:139-161 (linear_q / linear_k / linear_v,
+// apply_rope, and the K/V stores into the paged cache) with one launch, so
+// the projected K/V go from the MFMA accumulators to their cache slots
+// without a round trip through HBM.
+//
+// Semantics (bf16 model): q/k/v = x @ W^T with fp32 accumulation, rounded to
+// bf16 as F.linear stores them (gllm/model/layers/linear.py:13-19); q and k
+// rotated (rotate-half, every op rounded to bf16 like attention.py:105-118);
+// k and v cast to the cache dtype and stored at slot_mapping[token]
+// (attention.py:156-161), padded rows skipped; q written to q_out.
+//
+// Tiling: one 4-wave workgroup per (128 tokens, one head of D outputs).
+// X and W K-slices of 32 stream HBM/L2 -> LDS with global_load_lds into a
+// 4-stage ring (XOR-swizzled 16-byte chunks: operand reads are bank-conflict
+// free); each wave computes 32 tokens x D outputs on v_mfma_f32_32x32x16_bf16
+// (D/32 accumulator blocks).  Output column n of block b is head dim
+// 32b + n, so a RoPE pair (d, d + D/2) sits in blocks b and b + D/64 of the
+// same lane: the rotation happens in registers and every value is stored
+// from its lane (2-byte stores, 64-byte runs per half-wave).
+#include "common.h"
+#include "launch.h"
+
+namespace gllm {
+
+namespace {
+
+// One rotate-half pair, each op rounded to bf16 (attention.py:105-118).
+__device__ __forceinline__ void rope1_bf16(float& x1, float& x2, float c, float s) {
+  const float a = round_bf16(__fmul_rn(x1, c));
+  const float b = round_bf16(__fmul_rn(x2, s));
+  const float e = round_bf16(__fmul_rn(x1, s));
+  const float f = round_bf16(__fmul_rn(x2, c));
+  x1 = round_bf16(__fsub_rn(a, b));
+  x2 = round_bf16(__fadd_rn(e, f));
+}
+
+// Physical 16-byte chunk of logical chunk c in 64-byte LDS row r: rows
+// r, r+4, r+8, r+12 get the 4 chunk rotations, so 16 consecutive rows
+// reading one logical chunk hit 16 distinct bank groups.
+__device__ __forceinline__ int qkv_swz(int r) { return (r >> 2) & 3; }
+
+}  // namespace
+
+template <int D, bool KV8>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) qkv_rope_write_kernel(QKVArgs a) {
+  constexpr int TM = 128;                 // tokens per workgroup
+  constexpr int BK = 32;                  // K slice per stage
+  constexpr int NS = 4;                   // LDS ring stages
+  constexpr int NB = D / 32;              // accumulator blocks per wave (32 x 32 each)
+  constexpr int ROWB = BK * 2;            // 64-byte LDS rows
+  constexpr int A_BYTES = TM * ROWB;      // X slice
+  constexpr int B_BYTES = D * ROWB;       // W slice
+  constexpr int STAGE = A_BYTES + B_BYTES;
+  constexpr int IA = A_BYTES / (256 * 16);          // copy instructions per thread per stage: X
+  constexpr int IB = B_BYTES / (256 * 16);          //                                          W
+  constexpr int IPS = IA + IB;
+  static_assert(IA >= 1 && IB >= 1 && A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "tile / workgroup mismatch");
+  __shared__ __attribute__((aligned(16))) char lds[NS * STAGE];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int head = blockIdx.y;
+  const int kind = head < a.num_q_heads ? 0 : (head < a.num_q_heads + a.num_kv_heads ? 1 : 2);   // q, k, v
+  const int h = kind == 0 ? head : (kind == 1 ? head - a.num_q_heads : head - a.num_q_heads - a.num_kv_heads);
+  const char* w = (const char*)(kind == 0 ? a.w_q : (kind == 1 ? a.w_k : a.w_v));
+  const int64_t wstride = kind == 0 ? a.w_q_row_stride : (kind == 1 ? a.w_k_row_stride : a.w_v_row_stride);
+  w += (int64_t)h * D * wstride * 2;
+  const int64_t N = a.num_tokens;
+  const int64_t tok0 = (int64_t)blockIdx.x * TM;
+  const int nk = a.hidden / BK;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+
+  // Copy instruction i of this thread: 16-byte chunk c = i * 256 + tid of the
+  // stage's X (i < IA) or W part; LDS row c / 4, physical chunk c % 4, which
+  // holds logical chunk (c % 4) ^ qkv_swz(row).
+  auto dma = [&](int ks, int stage) {
+    const int64_t k0b = (int64_t)ks * BK * 2;
+#pragma unroll
+    for (int i = 0; i < IPS; ++i) {
+      const bool isA = i < IA;
+      const int c = (isA ? i : i - IA) * 256 + tid;
+      const int row = c >> 2, lc = (c & 3) ^ qkv_swz(row);
+      const char* src;
+      if (isA) {
+        const int64_t t = min(tok0 + row, N - 1);     // rows past the batch re-read the last token
+        src = (const char*)a.x + t * a.x_row_stride * 2 + k0b + lc * 16;
+      } else {
+        src = w + (int64_t)row * wstride * 2 + k0b + lc * 16;
+      }
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(
+          lds0 + stage * STAGE + (isA ? 0 : A_BYTES) + ((isA ? i : i - IA) * 256 + wave * 64) * 16);
+      lds_dma16(src, dst);
+    }
+  };
+
+  f32x16 acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[b][j] = 0.f;
+  const bool wact = tok0 + wave * 32 < N;     // this wave's 32 tokens hold at least one real one
+  const int ar = wave * 32 + (lane & 31);     // X row of the A operand
+  const int hi = lane >> 5;
+
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nk) dma(s, s);
+  for (int ks = 0; ks < nk; ++ks) {
+    // this thread's copies of stage ks are done once at most the copies of the
+    // (up to NS - 2) later stages already issued are outstanding
+    const int after = min(NS - 2, nk - 1 - ks);
+    if (after >= 2)
+      wait_vmcnt<2 * IPS>();
+    else if (after == 1)
+      wait_vmcnt<IPS>();
+    else
+      wait_vmcnt<0>();
+    __syncthreads();                           // stage ks visible; stage ks - 1 free
+    if (ks + NS - 1 < nk) dma(ks + NS - 1, (ks + NS - 1) % NS);
+    if (wact) {
+      const char* As = lds + (ks % NS) * STAGE;
+      const char* Bs = As + A_BYTES;
+#pragma unroll
+      for (int kk = 0; kk < BK / 16; ++kk) {
+        const int lc = 2 * kk + hi;
+        const bf16x8 av = __builtin_bit_cast(bf16x8, ld16(As + ar * ROWB + ((lc ^ qkv_swz(ar)) << 4)));
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const int br = 32 * b + (lane & 31);
+          const bf16x8 bv = __builtin_bit_cast(bf16x8, ld16(Bs + br * ROWB + ((lc ^ qkv_swz(br)) << 4)));
+          acc[b] = mfma32(av, bv, acc[b]);
+        }
+      }
+    }
+  }
+  if (!wact) return;
+
+  // Epilogue: lane holds C[token 8(j/4) + 4 hi + j%4][dim 32 b + lane % 32].
+  // Every per-token load (slot, cos/sin row, query length) and every cos/sin
+  // value is issued before the first store (the stores may alias them, so
+  // the compiler would otherwise serialise a round trip per token).
+  const int n = lane & 31;
+  const bool rope = kind == 1 || (kind == 0 && a.rotate_q);
+  constexpr int NH = NB / 2;
+  const int64_t tbase = tok0 + wave * 32 + 4 * hi;
+  int64_t dst[16];            // store offset per token (elements), -1: not written
+  uint32_t csn[16][NH];       // cos (low 16 bits) and sin (high) of the lane's rotation pairs
+  {
+    // loads first, each kind in its own loop (the conditions are uniform) and
+    // with the token index clamped into the batch, so they are in flight together
+    int64_t tc[16], crow[16], slot[16];
+    int32_t qlen[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      tc[j] = min(tbase + 8 * (j / 4) + (j % 4), N - 1);
+      crow[j] = tc[j];
+      slot[j] = 0;
+      qlen[j] = 0x7fffffff;
+    }
+    if (rope && a.rope_rows) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) crow[j] = a.rope_rows[tc[j]];
+    }
+    if (kind != 0) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) slot[j] = a.slot_mapping[tc[j]];
+      if (a.query_lens) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) qlen[j] = a.query_lens[tc[j] / a.tokens_per_seq];
+      }
+    }
+    if (rope) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint16_t* cp = (const uint16_t*)a.cos + crow[j] * a.rope_row_stride + n;
+        const uint16_t* sp = (const uint16_t*)a.sin + crow[j] * a.rope_row_stride + n;
+#pragma unroll
+        for (int b = 0; b < NH; ++b) csn[j][b] = (uint32_t)cp[32 * b] | ((uint32_t)sp[32 * b] << 16);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int64_t tok = tbase + 8 * (j / 4) + (j % 4);
+      int64_t d = -1;
+      if (tok < N) {
+        if (kind == 0) {
+          if (a.q_out) d = tok * a.q_out_row_stride + (int64_t)h * D;
+        } else {
+          // padded rows of the reference's [B, T_q] layout are not cached;
+          // slots outside the pool are never addressed
+          const bool real = !a.query_lens || tok % a.tokens_per_seq < qlen[j];
+          if (real && slot[j] >= 0 && slot[j] < a.num_slots) d = slot[j] * a.cache_slot_stride + (int64_t)h * D;
+        }
+      }
+      dst[j] = d;
+    }
+  }
+  char* base = (char*)(kind == 0 ? a.q_out : (kind == 1 ? a.k_cache : a.v_cache));
+  const bool to_cache = kind != 0;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    float v[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) v[b] = round_bf16(acc[b][j]);     // F.linear's bf16 output
+    if (rope) {
+#pragma unroll
+      for (int b = 0; b < NH; ++b)
+        rope1_bf16(v[b], v[b + NH], bf16_bits_to_f32(csn[j][b] & 0xffffu), bf16_bits_to_f32(csn[j][b] >> 16));
+    }
+    if (dst[j] < 0) continue;
+    if (KV8 && to_cache) {
+      char* cp = base + dst[j];
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+        *reinterpret_cast<uint8_t*>(cp + 32 * b + n) = (uint8_t)(pack_fp8x4(v[b], 0.f, 0.f, 0.f) & 0xffu);
+    } else {
+      char* cp = base + dst[j] * 2;
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+        *reinterpret_cast<uint16_t*>(cp + (32 * b + n) * 2) = (uint16_t)pack_bf16x2(v[b], 0.f);
+    }
+  }
+}
+
+hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t st) {
+  if (a.num_tokens == 0) return hipSuccess;
+  const int64_t tiles = (a.num_tokens + 127) / 128;
+  const int heads = (a.q_out ? a.num_q_heads : 0) + 2 * a.num_kv_heads;
+  if (tiles > 0x7fffffff || heads > 65535) return hipErrorInvalidValue;
+  // q heads are the first grid rows; without q_out the grid starts at the k heads
+  QKVArgs b = a;
+  if (!a.q_out) {
+    b.num_q_heads = 0;     // k heads become rows 0 .. Hkv - 1 (q weights unused)
+  }
+  const dim3 grid((unsigned)tiles, (unsigned)heads), block(256);
+  const bool kv8 = a.kv_dtype == kFP8;
+  if (a.head_dim == 64) {
+    if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<64, true>), grid, block, 0, st, b);
+    else hipLaunchKernelGGL((qkv_rope_write_kernel<64, false>), grid, block, 0, st, b);
+  } else if (a.head_dim == 128) {
+    if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<128, true>), grid, block, 0, st, b);
+    else hipLaunchKernelGGL((qkv_rope_write_kernel<128, false>), grid, block, 0, st, b);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace gllm

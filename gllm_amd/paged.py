@@ -89,6 +89,74 @@ def rope_kv_write(k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torc
         _lib.dtype_code(k.dtype), _lib.dtype_code(k_cache.dtype), _lib.stream_ptr(dev)))
 
 
+def qkv_rope_kv_write(x: torch.Tensor, w_q: torch.Tensor | None, w_k: torch.Tensor, w_v: torch.Tensor,
+                      cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                      slot_mapping: torch.Tensor, *, rotate_q: bool = True, q_out: torch.Tensor | None = None,
+                      query_lens: torch.Tensor | None = None, rope_rows: torch.Tensor | None = None):
+    """Fused ``linear_q/k/v`` + RoPE + KV-cache write of
+    ``gllm/model/layers/attention.py:139-161`` (bf16 model).
+
+    x ``[..., hidden]`` token rows; weights as the checkpoint stores them
+    (``w_q [Hq*D, hidden]``, ``w_k``/``w_v [Hkv*D, hidden]``, ``F.linear``
+    convention); caches ``[num_slots, Hkv, D]``; cos/sin / ``rope_rows`` /
+    ``query_lens`` / ``slot_mapping`` as in :func:`rope_kv_write`.  Returns q
+    ``[N, Hq, D]`` (rotated if ``rotate_q``) or None when ``w_q`` is None.
+    """
+    hidden = x.shape[-1]
+    xs = x.reshape(-1, hidden)
+    if xs.stride(-1) != 1:
+        raise ValueError("x rows must be contiguous")
+    n = xs.shape[0]
+    for t, nm in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        if t.dim() != 3 or t.stride(2) != 1 or t.stride(1) != t.shape[2]:
+            raise ValueError(f"{nm}: expected [num_slots, Hkv, D] with contiguous rows")
+    if k_cache.shape != v_cache.shape or k_cache.stride(0) != v_cache.stride(0):
+        raise ValueError("k_cache and v_cache must have the same shape and slot stride")
+    Hkv, D = k_cache.shape[1], k_cache.shape[2]
+    for w, nm in ((w_k, "w_k"), (w_v, "w_v")) + (((w_q, "w_q"),) if w_q is not None else ()):
+        if w.dim() != 2 or w.shape[1] != hidden or w.stride(1) != 1 or w.dtype != x.dtype:
+            raise ValueError(f"{nm}: expected [heads * D, {hidden}] with contiguous rows in the model dtype")
+    if w_k.shape[0] != Hkv * D or w_v.shape[0] != Hkv * D:
+        raise ValueError("w_k / w_v must have num_kv_heads * head_dim rows")
+    Hq = 0
+    if w_q is not None:
+        if w_q.shape[0] % D:
+            raise ValueError("w_q rows must be a multiple of head_dim")
+        Hq = w_q.shape[0] // D
+        if q_out is None:
+            q_out = torch.empty(n, Hq, D, dtype=x.dtype, device=x.device)
+        if q_out.reshape(-1, Hq * D).shape[0] != n or q_out.stride(-1) != 1:
+            raise ValueError("q_out must hold one contiguous row of Hq * D per token")
+    sm = slot_mapping.reshape(-1)
+    if sm.dtype != torch.int64 or sm.numel() != n or not sm.is_contiguous():
+        raise ValueError("slot_mapping must be contiguous int64 with one entry per token")
+    cs = cos.reshape(-1, cos.shape[-1])
+    sn = sin.reshape(-1, sin.shape[-1])
+    if cs.stride(-1) != 1 or sn.stride(-1) != 1 or cs.stride(0) != sn.stride(0):
+        raise ValueError("cos/sin must have contiguous rows of equal stride")
+    if cs.dtype != x.dtype or sn.dtype != x.dtype:
+        raise ValueError("cos/sin must be in the model dtype")
+    if cs.shape[-1] < D // 2 or (rope_rows is None and cs.shape[0] < n):
+        raise ValueError("cos/sin need one row of at least D/2 entries per token")
+    tps = 0
+    ql = None
+    if query_lens is not None:
+        ql = query_lens.to(torch.int32).contiguous()
+        tps = n // ql.numel()
+    rr = None
+    if rope_rows is not None:
+        rr = rope_rows.reshape(-1).to(torch.int64).contiguous()
+    lib = _lib.load()
+    qrow = q_out.reshape(-1, Hq * D).stride(0) if q_out is not None else 0
+    _lib.check(lib.gllm_qkv_rope_kv_write(
+        xs.data_ptr(), xs.stride(0), n, hidden, _lib.ptr(w_q), w_q.stride(0) if w_q is not None else 0,
+        w_k.data_ptr(), w_k.stride(0), w_v.data_ptr(), w_v.stride(0), _lib.ptr(q_out), qrow, int(bool(rotate_q)),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.shape[0], sm.data_ptr(), _lib.ptr(ql),
+        tps, cs.data_ptr(), sn.data_ptr(), _lib.ptr(rr), cs.stride(0), max(Hq, 1), Hkv, D,
+        _lib.dtype_code(x.dtype), _lib.dtype_code(k_cache.dtype), _lib.stream_ptr(x.device)))
+    return q_out
+
+
 def rope_rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                 rope_rows: torch.Tensor | None = None) -> torch.Tensor:
     """Rotate-half RoPE of ``x [..., H, D]`` (``attention.py:91-118``),

@@ -8,6 +8,9 @@
  *   gllm_rope_kv_write    replaces gllm/model/layers/attention.py:151-161
  *                         (Attention.apply_rope :76-119 on k [and q], then the
  *                         index_put_ of k/v through query_slot_mapping)
+ *   gllm_qkv_rope_kv_write replaces gllm/model/layers/attention.py:139-161
+ *                         (linear_q/k/v = F.linear, linear.py:13-19, then the
+ *                         same RoPE and KV write) with one fused launch
  *   gllm_paged_attention  replaces gllm/model/layers/attention.py:163-178
  *                         (the dense KV gather through slot_mapping plus
  *                         reference_attention with the 0/-inf bias of
@@ -81,6 +84,31 @@ int gllm_build_metadata(const int32_t* block_table, int64_t block_table_stride, 
                         const int32_t* seq_lens, const int32_t* query_lens, int32_t num_seqs,
                         int64_t q_seq_stride, int32_t block_size, int64_t* slot_mapping, int64_t* positions,
                         int32_t* cu_seqlens, int64_t num_rows, void* stream);
+
+/*
+ * Fused QKV projection + RoPE + paged KV write (bf16 model only; replaces
+ * attention.py:139-161).  For token t: q = x[t] @ w_q^T, k = x[t] @ w_k^T,
+ * v = x[t] @ w_v^T (w_* row-major [heads * head_dim, hidden] as the
+ * checkpoint stores them; fp32 accumulation, rounded to bf16 as F.linear
+ * stores its result), then k (and q if rotate_q) rotated exactly as
+ * gllm_rope_kv_write does and k/v stored at slot_mapping[t] in kv_dtype
+ * (bf16 or fp8 e4m3fn).  q is written to q_out if q_out != NULL (rotated or
+ * not: the paged attention kernels can rotate it on load).  query_lens /
+ * tokens_per_seq / rope_rows and the slot range check as in
+ * gllm_rope_kv_write.  hidden must be a positive multiple of 32; x, the
+ * weights and their row strides 16-byte aligned.  Results equal the
+ * reference within the GEMM's accumulation order (fp32 sums in another
+ * order, so a bf16 output may differ by one ulp); RoPE and the casts applied
+ * to those bf16 values are bit-identical.
+ */
+int gllm_qkv_rope_kv_write(const void* x, int64_t x_row_stride, int64_t num_tokens, int32_t hidden,
+                           const void* w_q, int64_t w_q_row_stride, const void* w_k, int64_t w_k_row_stride,
+                           const void* w_v, int64_t w_v_row_stride, void* q_out, int64_t q_out_row_stride,
+                           int32_t rotate_q, void* k_cache, void* v_cache, int64_t cache_slot_stride,
+                           int64_t num_slots, const int64_t* slot_mapping, const int32_t* query_lens,
+                           int64_t tokens_per_seq, const void* cos, const void* sin, const int64_t* rope_rows,
+                           int64_t rope_row_stride, int32_t num_q_heads, int32_t num_kv_heads,
+                           int32_t head_dim, int32_t dtype, int32_t kv_dtype, void* stream);
 
 /*
  * Rotate k (and, if q_out != NULL, q) with rotate-half RoPE and write k/v rows

@@ -1,0 +1,146 @@
+"""Fused QKV projection + RoPE + paged KV write (gllm/model/layers/attention.py:139-161)
+against the oracle restatement.
+
+The GEMM accumulates in fp32 in its own order, so a projected bf16 value may
+differ from the correctly rounded one by one unit in the last place near a
+rounding boundary (torch's own bf16 F.linear does the same); random-data
+cases allow that on a small fraction of values.  With small-integer data
+every dot product is exact in fp32 and bf16, so those cases pin the RoPE,
+the casts and the slot writes bit for bit."""
+import pytest
+import torch
+
+from gllm_amd import paged
+from oracle import projection as op
+from oracle import rope as orope
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF = torch.bfloat16
+
+
+def _inputs(n, hidden, Hq, Hkv, D, integer, seed, theta=500000.0, max_pos=4096):
+    g = torch.Generator().manual_seed(seed)
+    if integer:
+        x = torch.randint(-1, 2, (n, hidden), generator=g).to(BF)
+        w = [torch.randint(-1, 2, (h * D, hidden), generator=g).to(BF) for h in (Hq, Hkv, Hkv)]
+    else:
+        x = torch.randn(n, hidden, generator=g).to(BF)
+        w = [(torch.randn(h * D, hidden, generator=g) / hidden ** 0.5).to(BF) for h in (Hq, Hkv, Hkv)]
+    cos_t, sin_t = orope.rope_cache(max_pos, D, theta, BF)
+    pos = torch.randint(0, max_pos, (n,), generator=g)
+    num_slots = 2 * n + 16
+    slots = torch.randperm(num_slots, generator=g)[:n].to(torch.int64)
+    return x, w, cos_t, sin_t, pos, slots, num_slots
+
+
+def _pair_norm(t):
+    """|(x_d, x_{d+D/2})| per element: the rotation keeps it, so it bounds
+    the error a one-ulp difference of the projected pair leaves after RoPE."""
+    h = t.shape[-1] // 2
+    r = (t[..., :h] ** 2 + t[..., h:] ** 2).sqrt()
+    return torch.cat([r, r], -1)
+
+
+def _close_bf16(got, want, what, rotated, frac=0.02):
+    got, want = got.float().cpu(), want.float().cpu()
+    diff = (got - want).abs()
+    # a one-ulp difference of a projected value goes through RoPE's three
+    # roundings: up to ~3 ulps of the pair's magnitude (4 allowed); v: 2 ulps
+    if rotated:
+        tol = torch.maximum(_pair_norm(got), _pair_norm(want)) * 2 ** -6 + 1e-6
+    else:
+        tol = torch.maximum(got.abs(), want.abs()) * 2 ** -7 + 1e-6
+    assert bool((diff <= tol).all()), f"{what}: max diff {diff.max().item()} (worst ratio {(diff / tol).max().item():.2f})"
+    assert (got != want).float().mean().item() <= frac, f"{what}: {(got != want).float().mean().item():.4f} differ"
+
+
+def _run(n, hidden, Hq, Hkv, D, integer, seed, kv_dtype=BF, rotate_q=True, with_q=True):
+    x, (wq, wk, wv), cos_t, sin_t, pos, slots, ns = _inputs(n, hidden, Hq, Hkv, D, integer, seed)
+    sentinel = 3.0
+    kc = torch.full((ns, Hkv, D), sentinel, dtype=BF).to(kv_dtype)
+    vc = kc.clone()
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    q = paged.qkv_rope_kv_write(x.to(DEV), wq.to(DEV) if with_q else None, wk.to(DEV), wv.to(DEV),
+                                cos_t.to(DEV), sin_t.to(DEV), kcg := kc.to(DEV), vcg := vc.to(DEV),
+                                slots.to(DEV), rotate_q=rotate_q, rope_rows=pos.to(DEV))
+    torch.cuda.synchronize()
+    qr = op.qkv_rope_kv_write(x, wq, wk, wv, cos_t[pos], sin_t[pos], kc_ref, vc_ref, slots, Hkv, D)
+    if not rotate_q:
+        qr = op.linear(x, wq).view(n, Hq, D)
+    return q, qr, kcg.cpu(), vcg.cpu(), kc_ref, vc_ref, slots, ns
+
+
+@pytest.mark.parametrize("n,hidden,Hq,Hkv,D", [(1, 128, 4, 2, 64), (130, 128, 8, 2, 128), (300, 256, 16, 4, 64),
+                                               (77, 96, 4, 4, 128)])
+def test_qkv_exact_on_integer_data(n, hidden, Hq, Hkv, D):
+    """Exact GEMM (small integers): q, the cached k (rotated) and v bit-exact,
+    untouched slots keep their sentinel."""
+    print(f"qkv exact n={n} hidden={hidden} Hq={Hq} Hkv={Hkv} D={D}", flush=True)
+    q, qr, kc, vc, kr, vr, slots, ns = _run(n, hidden, Hq, Hkv, D, True, 11 + n)
+    assert torch.equal(q.cpu().view(torch.int16), qr.view(torch.int16))
+    assert torch.equal(kc.view(torch.int16), kr.view(torch.int16))
+    assert torch.equal(vc.view(torch.int16), vr.view(torch.int16))
+
+
+@pytest.mark.parametrize("n,hidden,Hq,Hkv,D", [(64, 2048, 32, 8, 64), (259, 4096, 32, 8, 128),
+                                               (131, 1024, 8, 1, 128), (5, 512, 16, 16, 64)])
+def test_qkv_random_data(n, hidden, Hq, Hkv, D):
+    """Llama-shaped projections (1B: hidden 2048 / D 64; 8B: 4096 / 128) on
+    N(0,1) data: within the GEMM's accumulation-order rounding."""
+    print(f"qkv random n={n} hidden={hidden} Hq={Hq} Hkv={Hkv} D={D}", flush=True)
+    q, qr, kc, vc, kr, vr, slots, ns = _run(n, hidden, Hq, Hkv, D, False, 3 + n)
+    _close_bf16(q, qr, "q", True)
+    _close_bf16(kc[slots], kr[slots], "k", True)
+    _close_bf16(vc[slots], vr[slots], "v", False)
+    rest = torch.ones(ns, dtype=torch.bool)
+    rest[slots] = False
+    assert bool((kc[rest] == 3.0).all()) and bool((vc[rest] == 3.0).all())
+
+
+def test_qkv_unrotated_q_and_fp8_cache():
+    """rotate_q=False writes the plain projection (the attention kernels rotate
+    q on load); an fp8 cache gets the rounded-like-torch cast of the bf16
+    values (exact data, so byte-exact)."""
+    print("qkv unrotated q, fp8 cache", flush=True)
+    f8 = torch.float8_e4m3fn
+    q, qr, kc, vc, kr, vr, slots, ns = _run(90, 128, 8, 2, 64, True, 21, kv_dtype=f8, rotate_q=False)
+    assert torch.equal(q.cpu().view(torch.int16), qr.view(torch.int16))
+    assert torch.equal(kc.view(torch.uint8), kr.view(torch.uint8))
+    assert torch.equal(vc.view(torch.uint8), vr.view(torch.uint8))
+
+
+def test_qkv_without_q_and_padded_rows():
+    """w_q=None skips the q heads; query_lens skips the reference's padded
+    rows of a [B, T_q] layout (left in the cache as they were)."""
+    print("qkv no q, padded rows", flush=True)
+    B, Tq, hidden, Hkv, D = 3, 20, 128, 2, 128
+    n = B * Tq
+    x, (wq, wk, wv), cos_t, sin_t, pos, slots, ns = _inputs(n, hidden, 4, Hkv, D, True, 31)
+    ql = torch.tensor([20, 7, 1], dtype=torch.int32)
+    kc = torch.full((ns, Hkv, D), 3.0, dtype=BF)
+    vc = kc.clone()
+    kg, vg = kc.to(DEV), vc.to(DEV)
+    out = paged.qkv_rope_kv_write(x.to(DEV), None, wk.to(DEV), wv.to(DEV), cos_t.to(DEV), sin_t.to(DEV), kg, vg,
+                                  slots.to(DEV), query_lens=ql.to(DEV), rope_rows=pos.to(DEV))
+    torch.cuda.synchronize()
+    assert out is None
+    real = (torch.arange(n) % Tq) < ql.repeat_interleave(Tq)
+    op.qkv_rope_kv_write(x, None, wk, wv, cos_t[pos], sin_t[pos], kc, vc, slots, Hkv, D, real=real)
+    assert torch.equal(kg.cpu().view(torch.int16), kc.view(torch.int16))
+    assert torch.equal(vg.cpu().view(torch.int16), vc.view(torch.int16))
+
+
+def test_qkv_rejects_bad_arguments():
+    print("qkv errors", flush=True)
+    x = torch.zeros(4, 100, dtype=BF, device=DEV)          # hidden not a multiple of 32
+    w = torch.zeros(128, 100, dtype=BF, device=DEV)
+    kc = torch.zeros(16, 1, 128, dtype=BF, device=DEV)
+    cs = torch.zeros(4, 64, dtype=BF, device=DEV)
+    sl = torch.arange(4, dtype=torch.int64, device=DEV)
+    with pytest.raises(NotImplementedError):
+        paged.qkv_rope_kv_write(x, None, w, w, cs, cs, kc, kc.clone(), sl)
+    x32 = torch.zeros(4, 128, dtype=torch.float32, device=DEV)
+    w32 = torch.zeros(128, 128, dtype=torch.float32, device=DEV)
+    with pytest.raises(NotImplementedError):
+        paged.qkv_rope_kv_write(x32, None, w32, w32, cs.float(), cs.float(), kc.float(), kc.float().clone(), sl)
