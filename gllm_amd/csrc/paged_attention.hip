@@ -686,6 +686,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 
   const float sl2 = a.scale * kLog2e;
   float m = kNegInf, lsum = 0.f;
+  float sbase = 0.f;             // value the tile's S accumulators start from
   f32x16 o[NO];
 #pragma unroll
   for (int db = 0; db < NO; ++db)
@@ -697,18 +698,21 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   // sm_max: mask, row max, running-max update (lazy rescale: the max only
   // moves when a row's max exceeds it by more than 8 in log2 units, so
   // p <= 2^8; numerator and denominator share m, so the result is exact);
-  // sm_exp: p = 2^(s sl2 - m) for 4 scores; sm_sum: row sum; sm_cvt: P as two
-  // bf16 B operands.
-  struct Soft { float alpha, nmu, psum; };
+  // sm_exp: p = 2^(s - m) for 4 scores; sm_sum: row sum; sm_cvt: P as two
+  // bf16 B operands.  Q is pre-scaled by scale * log2(e) and the S
+  // accumulators start at -m (the running max when the tile begins, 0 while
+  // it is -inf), so the MFMA yields s = q.k scale log2(e) - m directly: the
+  // exponent needs no per-score FMA while the max stays put (a subtract of
+  // the max's move otherwise, rare with the lazy rescale).
+  struct Soft { float alpha, dlt, psum; };
   auto sm_max = [&](f32x16& s, int k0, bool mask, Soft& q) {
     if (DENSE) {
       const __bf16* bp = (const __bf16*)a.bias + (int64_t)seq * a.bias_batch_stride + (int64_t)rr * a.bias_row_stride;
-      const float inv_scale = 1.f / a.scale;   // bias is added in natural-log units
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
+      for (int j = 0; j < 16; ++j) {   // bias in natural-log units: to log2 units like the scaled scores
         const int key = k0 + 8 * (j >> 2) + 4 * h + (j & 3);
         const float bv = key < T ? (float)bp[key] : kNegInf;
-        s[j] = __builtin_fmaf(bv, inv_scale, s[j]);
+        s[j] = __builtin_fmaf(bv, kLog2e, s[j]);
       }
     } else if (mask) {
 #pragma unroll
@@ -723,16 +727,21 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
       tmax = __builtin_elementwise_maximum(tmax, __builtin_elementwise_maximum(s[j], s[j + 1]));
     {
       auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
-      tmax = __builtin_elementwise_maximum(__uint_as_float(x[0]), __uint_as_float(x[1])) * sl2;
+      tmax = __builtin_elementwise_maximum(__uint_as_float(x[0]), __uint_as_float(x[1])) - sbase;
     }
     const float mn = tmax > m + 8.f ? tmax : m;
     q.alpha = mn > m ? fast_exp2(m - mn) : 1.f;
     m = mn;
-    q.nmu = mn == kNegInf ? 0.f : -mn;
+    // s holds s_true + sbase; the exponent is s_true - m = s - (sbase + m)
+    q.dlt = mn == kNegInf ? 0.f : sbase + mn;
+    if (__builtin_amdgcn_ballot_w64(q.dlt != 0.f)) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) s[j] -= q.dlt;
+    }
   };
   auto sm_exp = [&](f32x16& s, int j0, const Soft& q) {
 #pragma unroll
-    for (int j = j0; j < j0 + 4; ++j) s[j] = fast_exp2(__builtin_fmaf(s[j], sl2, q.nmu));
+    for (int j = j0; j < j0 + 4; ++j) s[j] = fast_exp2(s[j]);
   };
   auto sm_sum = [&](const f32x16& s, Soft& q) {
     float ps4[4];
@@ -790,8 +799,9 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int kk = 0; kk < NQ; ++kk) ka[kb][kk] = *reinterpret_cast<const u32x4*>(st + kb * 32 * RW + koff[kk]);
+    sbase = m == kNegInf ? 0.f : -m;     // both halves start from the max before this tile
 #pragma unroll
-    for (int j = 0; j < 16; ++j) s0[j] = 0.f, s1[j] = 0.f;
+    for (int j = 0; j < 16; ++j) s0[j] = sbase, s1[j] = sbase;
 #pragma unroll
     for (int kk = 0; kk < NQ; ++kk) s0 = mfma32(as_bf16x8(ka[0][kk]), qB[kk], s0);
     // region 1: S^T half 1 | V reads half 0 | softmax half 0
@@ -883,7 +893,11 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
       }
     }
 #pragma unroll
-    for (int kk = 0; kk < NQ; ++kk) qB[kk] = to_bf16x8(x[kk]);
+    for (int kk = 0; kk < NQ; ++kk) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[kk][i] *= sl2;     // scores come out in log2 units
+      qB[kk] = to_bf16x8(x[kk]);
+    }
   }
 
   for (int t0 = 0; t0 < ntiles; t0 += TPB) {
