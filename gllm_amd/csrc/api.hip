@@ -48,6 +48,16 @@ int log2i(int64_t x) {
 }
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// Compute units of the current device (256 when there is none, e.g. a CPU-only host).
+int device_cus() {
+  int dev = 0;
+  hipDeviceProp_t prop;
+  if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0)
+    return prop.multiProcessorCount;
+  (void)hipGetLastError();
+  return 256;
+}
+
 }  // namespace
 
 struct gllm_attn_plan {
@@ -241,7 +251,8 @@ int gllm_qkv_rope_kv_write(const void* x, int64_t x_row_stride, int64_t num_toke
                            int64_t num_slots, const int64_t* slot_mapping, const int32_t* query_lens,
                            int64_t tokens_per_seq, const void* cos, const void* sin, const int64_t* rope_rows,
                            int64_t rope_row_stride, int32_t num_q_heads, int32_t num_kv_heads,
-                           int32_t head_dim, int32_t dtype, int32_t kv_dtype, void* stream) {
+                           int32_t head_dim, int32_t dtype, int32_t kv_dtype, void* workspace,
+                           size_t workspace_bytes, void* stream) {
   if (num_tokens < 0) return fail(GLLM_ATTN_EINVAL, "num_tokens < 0");
   if (dtype != GLLM_DTYPE_BF16) return fail(GLLM_ATTN_EUNSUPPORTED, "fused QKV projection needs a bf16 model (dtype %d)", dtype);
   if (kv_dtype != GLLM_DTYPE_BF16 && kv_dtype != GLLM_DTYPE_FP8_E4M3)
@@ -273,7 +284,17 @@ int gllm_qkv_rope_kv_write(const void* x, int64_t x_row_stride, int64_t num_toke
   a.slot_mapping = slot_mapping; a.query_lens = query_lens; a.tokens_per_seq = tokens_per_seq;
   a.cos = cos; a.sin = sin; a.rope_rows = rope_rows; a.rope_row_stride = rope_row_stride;
   a.num_q_heads = num_q_heads; a.num_kv_heads = num_kv_heads; a.head_dim = head_dim; a.kv_dtype = kv_dtype;
+  if (workspace && ((uintptr_t)workspace & 15)) return fail(GLLM_ATTN_EINVAL, "workspace must be 16-byte aligned");
+  a.workspace = (float*)workspace; a.workspace_bytes = workspace ? workspace_bytes : 0;
+  a.cus = device_cus();
   return hip_check(launch_qkv_rope_write(a, (hipStream_t)stream), "qkv projection launch");
+}
+
+size_t gllm_qkv_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t num_q_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int32_t with_q) {
+  if (num_tokens <= 0 || hidden <= 0 || num_kv_heads <= 0 || num_q_heads < 0) return 0;
+  return qkv_workspace_bytes(num_tokens, hidden, (with_q ? num_q_heads : 0) + 2 * num_kv_heads, head_dim,
+                             device_cus());
 }
 
 int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const int32_t* seq_lens,

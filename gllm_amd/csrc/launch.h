@@ -122,7 +122,14 @@ struct QKVArgs {
   int64_t rope_row_stride;
   int32_t num_q_heads, num_kv_heads, head_dim;
   int32_t kv_dtype;
+  // split-K path (few tokens): fp32 partials [split_count][num_tokens][heads * D]
+  float* workspace;
+  size_t workspace_bytes;
+  int32_t cus;                   // compute units (planning)
+  int32_t split_chunk, split_count;
 };
+
+size_t qkv_workspace_bytes(int64_t num_tokens, int hidden, int heads, int head_dim, int cus);
 
 hipError_t launch_rope_kv_write(const RopeKVWriteArgs& a, hipStream_t stream);
 hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t stream);

@@ -17,7 +17,11 @@
 // (D/32 accumulator blocks).  Output column n of block b is head dim
 // 32b + n, so a RoPE pair (d, d + D/2) sits in blocks b and b + D/64 of the
 // same lane: the rotation happens in registers and every value is stored
-// from its lane (2-byte stores, 64-byte runs per half-wave).
+// from its lane (2-byte stores, 64-byte runs per half-wave).  Batches too
+// small to fill the GPU with such tiles split the hidden dimension
+// (qkv_partial_kernel + qkv_finish_kernel, below).
+#include <algorithm>
+
 #include "common.h"
 #include "launch.h"
 
@@ -222,6 +226,182 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) q
   }
 }
 
+// ------------------------------------------------------------------ split-K
+// Batches of few tokens (decode) give the tile kernel too few workgroups to
+// stream the weights at full bandwidth.  There the K range is split: each
+// workgroup computes fp32 partial sums of 64 tokens x one head over one K
+// chunk (plain vector stores into the caller's workspace,
+// [chunk][token][head * D + d]); qkv_finish_kernel sums the chunks in fixed
+// order (deterministic), rounds like F.linear and does the RoPE and the
+// stores exactly as the tile kernel's epilogue.
+template <int D>
+__global__ void __launch_bounds__(256) qkv_partial_kernel(QKVArgs a) {
+  constexpr int TM = 64;                  // tokens per workgroup (waves: 2 token blocks x 2 output halves)
+  constexpr int BK = 32;
+  constexpr int NS = 4;
+  constexpr int NBW = D / 64;             // 32 x 32 blocks per wave (D/2 outputs)
+  constexpr int ROWB = BK * 2;
+  constexpr int A_BYTES = TM * ROWB;      // 4 KB
+  constexpr int B_BYTES = D * ROWB;
+  constexpr int STAGE = A_BYTES + B_BYTES;
+  constexpr int IA = A_BYTES / (256 * 16);
+  constexpr int IB = B_BYTES / (256 * 16);
+  constexpr int IPS = IA + IB;
+  static_assert(IA == 1 && IB >= 1, "tile / workgroup mismatch");
+  __shared__ __attribute__((aligned(16))) char lds[NS * STAGE];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int head = blockIdx.y;
+  const int kind = head < a.num_q_heads ? 0 : (head < a.num_q_heads + a.num_kv_heads ? 1 : 2);
+  const int h = kind == 0 ? head : (kind == 1 ? head - a.num_q_heads : head - a.num_q_heads - a.num_kv_heads);
+  const char* w = (const char*)(kind == 0 ? a.w_q : (kind == 1 ? a.w_k : a.w_v));
+  const int64_t wstride = kind == 0 ? a.w_q_row_stride : (kind == 1 ? a.w_k_row_stride : a.w_v_row_stride);
+  w += (int64_t)h * D * wstride * 2;
+  const int64_t N = a.num_tokens;
+  const int64_t tok0 = (int64_t)blockIdx.x * TM;
+  const int kc0 = blockIdx.z * a.split_chunk;
+  const int nk = min(a.split_chunk, a.hidden - kc0) / BK;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+
+  auto dma = [&](int ks, int stage) {
+    const int64_t k0b = (int64_t)(kc0 + ks * BK) * 2;
+#pragma unroll
+    for (int i = 0; i < IPS; ++i) {
+      const bool isA = i < IA;
+      const int c = (isA ? i : i - IA) * 256 + tid;
+      const int row = c >> 2, lc = (c & 3) ^ qkv_swz(row);
+      const char* src;
+      if (isA) {
+        const int64_t t = min(tok0 + row, N - 1);
+        src = (const char*)a.x + t * a.x_row_stride * 2 + k0b + lc * 16;
+      } else {
+        src = w + (int64_t)row * wstride * 2 + k0b + lc * 16;
+      }
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(
+          lds0 + stage * STAGE + (isA ? 0 : A_BYTES) + ((isA ? i : i - IA) * 256 + wave * 64) * 16);
+      lds_dma16(src, dst);
+    }
+  };
+
+  f32x16 acc[NBW];
+#pragma unroll
+  for (int b = 0; b < NBW; ++b)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[b][j] = 0.f;
+  const int tb = wave & 1, fh = wave >> 1;
+  const bool wact = tok0 + tb * 32 < N;
+  const int ar = tb * 32 + (lane & 31);
+  const int hi = lane >> 5;
+
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nk) dma(s, s);
+  for (int ks = 0; ks < nk; ++ks) {
+    const int after = min(NS - 2, nk - 1 - ks);
+    if (after >= 2)
+      wait_vmcnt<2 * IPS>();
+    else if (after == 1)
+      wait_vmcnt<IPS>();
+    else
+      wait_vmcnt<0>();
+    __syncthreads();
+    if (ks + NS - 1 < nk) dma(ks + NS - 1, (ks + NS - 1) % NS);
+    if (wact) {
+      const char* As = lds + (ks % NS) * STAGE;
+      const char* Bs = As + A_BYTES;
+#pragma unroll
+      for (int kk = 0; kk < BK / 16; ++kk) {
+        const int lc = 2 * kk + hi;
+        const bf16x8 av = __builtin_bit_cast(bf16x8, ld16(As + ar * ROWB + ((lc ^ qkv_swz(ar)) << 4)));
+#pragma unroll
+        for (int b = 0; b < NBW; ++b) {
+          const int br = fh * (D / 2) + 32 * b + (lane & 31);
+          const bf16x8 bv = __builtin_bit_cast(bf16x8, ld16(Bs + br * ROWB + ((lc ^ qkv_swz(br)) << 4)));
+          acc[b] = mfma32(av, bv, acc[b]);
+        }
+      }
+    }
+  }
+  if (!wact) return;
+  const int64_t F = (int64_t)(a.num_q_heads + 2 * a.num_kv_heads) * D;
+  float* ws = a.workspace + (int64_t)blockIdx.z * N * F + (int64_t)head * D + fh * (D / 2) + (lane & 31);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int64_t tok = tok0 + tb * 32 + 8 * (j / 4) + 4 * hi + (j % 4);
+    if (tok >= N) continue;
+#pragma unroll
+    for (int b = 0; b < NBW; ++b) ws[tok * F + 32 * b] = acc[b][j];
+  }
+}
+
+// One thread per rotation pair (d, d + D/2) of one (token, head).
+template <int D, bool KV8>
+__global__ void __launch_bounds__(256) qkv_finish_kernel(QKVArgs a) {
+  constexpr int PPH = D / 2;              // pairs per head
+  constexpr int HPB = 256 / PPH;          // heads per workgroup
+  const int heads = a.num_q_heads + 2 * a.num_kv_heads;
+  const int64_t tok = blockIdx.x;
+  const int head = blockIdx.y * HPB + threadIdx.x / PPH;
+  const int d = threadIdx.x % PPH;
+  if (head >= heads) return;
+  const int kind = head < a.num_q_heads ? 0 : (head < a.num_q_heads + a.num_kv_heads ? 1 : 2);
+  const int h = kind == 0 ? head : (kind == 1 ? head - a.num_q_heads : head - a.num_q_heads - a.num_kv_heads);
+  const int64_t F = (int64_t)heads * D;
+  const float* ws = a.workspace + tok * F + (int64_t)head * D + d;
+  float x1 = 0.f, x2 = 0.f;
+  for (int c = 0; c < a.split_count; ++c) {   // chunk order fixed: deterministic sums
+    x1 += ws[(int64_t)c * a.num_tokens * F];
+    x2 += ws[(int64_t)c * a.num_tokens * F + PPH];
+  }
+  x1 = round_bf16(x1);
+  x2 = round_bf16(x2);
+  if (kind == 1 || (kind == 0 && a.rotate_q)) {
+    const int64_t crow = a.rope_rows ? a.rope_rows[tok] : tok;
+    const float c = bf16_bits_to_f32(((const uint16_t*)a.cos)[crow * a.rope_row_stride + d]);
+    const float sn = bf16_bits_to_f32(((const uint16_t*)a.sin)[crow * a.rope_row_stride + d]);
+    rope1_bf16(x1, x2, c, sn);
+  }
+  if (kind == 0) {
+    uint16_t* op = (uint16_t*)a.q_out + tok * a.q_out_row_stride + (int64_t)h * D + d;
+    op[0] = (uint16_t)pack_bf16x2(x1, 0.f);
+    op[PPH] = (uint16_t)pack_bf16x2(x2, 0.f);
+    return;
+  }
+  if (a.query_lens && tok % a.tokens_per_seq >= a.query_lens[tok / a.tokens_per_seq]) return;
+  const int64_t slot = a.slot_mapping[tok];
+  if (slot < 0 || slot >= a.num_slots) return;
+  char* cp = (char*)(kind == 1 ? a.k_cache : a.v_cache) + (slot * a.cache_slot_stride + (int64_t)h * D + d) * (KV8 ? 1 : 2);
+  if (KV8) {
+    cp[0] = (char)(pack_fp8x4(x1, 0.f, 0.f, 0.f) & 0xffu);
+    cp[PPH] = (char)(pack_fp8x4(x2, 0.f, 0.f, 0.f) & 0xffu);
+  } else {
+    *reinterpret_cast<uint16_t*>(cp) = (uint16_t)pack_bf16x2(x1, 0.f);
+    *reinterpret_cast<uint16_t*>(cp + PPH * 2) = (uint16_t)pack_bf16x2(x2, 0.f);
+  }
+}
+
+// Split-K plan for a batch: chunk length (multiple of 32, >= 256) and count,
+// or count 1 when the tile kernel already has enough workgroups.
+static void qkv_split_plan(int64_t n, int hidden, int heads, int cus, int* chunk, int* count) {
+  *chunk = hidden;
+  *count = 1;
+  const int64_t tiles = (n + 127) / 128;
+  if (n == 0 || tiles * heads >= cus || hidden < 512) return;
+  const int64_t wgs64 = ((n + 63) / 64) * heads;
+  int64_t want = (2 * (int64_t)cus + wgs64 - 1) / wgs64;           // about two workgroups per CU
+  want = std::min<int64_t>(std::min<int64_t>(want, hidden / 256), 16);   // the finish kernel sums <= 16 chunks
+  if (want <= 1) return;
+  const int c = (int)(((hidden + want - 1) / want + 31) / 32 * 32);
+  *chunk = c;
+  *count = (hidden + c - 1) / c;
+}
+
+size_t qkv_workspace_bytes(int64_t n, int hidden, int heads, int head_dim, int cus) {
+  int chunk, count;
+  qkv_split_plan(n, hidden, heads, cus, &chunk, &count);
+  return count > 1 ? (size_t)count * n * heads * head_dim * sizeof(float) : 0;
+}
+
 hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t st) {
   if (a.num_tokens == 0) return hipSuccess;
   const int64_t tiles = (a.num_tokens + 127) / 128;
@@ -229,11 +409,30 @@ hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t st) {
   if (tiles > 0x7fffffff || heads > 65535) return hipErrorInvalidValue;
   // q heads are the first grid rows; without q_out the grid starts at the k heads
   QKVArgs b = a;
-  if (!a.q_out) {
-    b.num_q_heads = 0;     // k heads become rows 0 .. Hkv - 1 (q weights unused)
+  if (!a.q_out) b.num_q_heads = 0;
+  const bool kv8 = a.kv_dtype == kFP8;
+  int chunk, count;
+  qkv_split_plan(a.num_tokens, a.hidden, heads, a.cus, &chunk, &count);
+  if (count > 1 && a.workspace &&
+      a.workspace_bytes >= (size_t)count * a.num_tokens * heads * a.head_dim * sizeof(float)) {
+    b.split_chunk = chunk;
+    b.split_count = count;
+    const dim3 g1((unsigned)((a.num_tokens + 63) / 64), (unsigned)heads, (unsigned)count), blk(256);
+    const dim3 g2((unsigned)a.num_tokens, (unsigned)((heads + 256 / (a.head_dim / 2) - 1) / (256 / (a.head_dim / 2))));
+    if (a.head_dim == 64) {
+      hipLaunchKernelGGL((qkv_partial_kernel<64>), g1, blk, 0, st, b);
+      if (kv8) hipLaunchKernelGGL((qkv_finish_kernel<64, true>), g2, blk, 0, st, b);
+      else hipLaunchKernelGGL((qkv_finish_kernel<64, false>), g2, blk, 0, st, b);
+    } else if (a.head_dim == 128) {
+      hipLaunchKernelGGL((qkv_partial_kernel<128>), g1, blk, 0, st, b);
+      if (kv8) hipLaunchKernelGGL((qkv_finish_kernel<128, true>), g2, blk, 0, st, b);
+      else hipLaunchKernelGGL((qkv_finish_kernel<128, false>), g2, blk, 0, st, b);
+    } else {
+      return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
   }
   const dim3 grid((unsigned)tiles, (unsigned)heads), block(256);
-  const bool kv8 = a.kv_dtype == kFP8;
   if (a.head_dim == 64) {
     if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<64, true>), grid, block, 0, st, b);
     else hipLaunchKernelGGL((qkv_rope_write_kernel<64, false>), grid, block, 0, st, b);

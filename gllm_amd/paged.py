@@ -92,7 +92,8 @@ def rope_kv_write(k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torc
 def qkv_rope_kv_write(x: torch.Tensor, w_q: torch.Tensor | None, w_k: torch.Tensor, w_v: torch.Tensor,
                       cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                       slot_mapping: torch.Tensor, *, rotate_q: bool = True, q_out: torch.Tensor | None = None,
-                      query_lens: torch.Tensor | None = None, rope_rows: torch.Tensor | None = None):
+                      query_lens: torch.Tensor | None = None, rope_rows: torch.Tensor | None = None,
+                      split_k: bool = True):
     """Fused ``linear_q/k/v`` + RoPE + KV-cache write of
     ``gllm/model/layers/attention.py:139-161`` (bf16 model).
 
@@ -101,6 +102,8 @@ def qkv_rope_kv_write(x: torch.Tensor, w_q: torch.Tensor | None, w_k: torch.Tens
     convention); caches ``[num_slots, Hkv, D]``; cos/sin / ``rope_rows`` /
     ``query_lens`` / ``slot_mapping`` as in :func:`rope_kv_write`.  Returns q
     ``[N, Hq, D]`` (rotated if ``rotate_q``) or None when ``w_q`` is None.
+    ``split_k``: let batches of few tokens split the hidden dimension over
+    more workgroups (a cached device workspace); False forces the tile kernel.
     """
     hidden = x.shape[-1]
     xs = x.reshape(-1, hidden)
@@ -148,13 +151,29 @@ def qkv_rope_kv_write(x: torch.Tensor, w_q: torch.Tensor | None, w_k: torch.Tens
         rr = rope_rows.reshape(-1).to(torch.int64).contiguous()
     lib = _lib.load()
     qrow = q_out.reshape(-1, Hq * D).stride(0) if q_out is not None else 0
+    wsb = lib.gllm_qkv_workspace_bytes(n, hidden, max(Hq, 1), Hkv, D, int(w_q is not None)) if split_k else 0
+    ws = _qkv_workspace(x.device, wsb) if wsb else None
     _lib.check(lib.gllm_qkv_rope_kv_write(
         xs.data_ptr(), xs.stride(0), n, hidden, _lib.ptr(w_q), w_q.stride(0) if w_q is not None else 0,
         w_k.data_ptr(), w_k.stride(0), w_v.data_ptr(), w_v.stride(0), _lib.ptr(q_out), qrow, int(bool(rotate_q)),
         k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.shape[0], sm.data_ptr(), _lib.ptr(ql),
         tps, cs.data_ptr(), sn.data_ptr(), _lib.ptr(rr), cs.stride(0), max(Hq, 1), Hkv, D,
-        _lib.dtype_code(x.dtype), _lib.dtype_code(k_cache.dtype), _lib.stream_ptr(x.device)))
+        _lib.dtype_code(x.dtype), _lib.dtype_code(k_cache.dtype), _lib.ptr(ws), wsb, _lib.stream_ptr(x.device)))
     return q_out
+
+
+_QKV_WS: dict = {}
+
+
+def _qkv_workspace(device, nbytes: int) -> torch.Tensor:
+    """Per-device scratch for the split-K projection (grown on demand, kept;
+    fully rewritten by every call, so never cleared)."""
+    key = torch.device(device)
+    ws = _QKV_WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=key)
+        _QKV_WS[key] = ws
+    return ws
 
 
 def rope_rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,

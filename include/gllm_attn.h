@@ -96,7 +96,8 @@ int gllm_build_metadata(const int32_t* block_table, int64_t block_table_stride, 
  * not: the paged attention kernels can rotate it on load).  query_lens /
  * tokens_per_seq / rope_rows and the slot range check as in
  * gllm_rope_kv_write.  hidden must be a positive multiple of 32; x, the
- * weights and their row strides 16-byte aligned.  Results equal the
+ * weights and their row strides 16-byte aligned.  workspace (may be NULL,
+ * 16-byte aligned) see gllm_qkv_workspace_bytes.  Results equal the
  * reference within the GEMM's accumulation order (fp32 sums in another
  * order, so a bf16 output may differ by one ulp); RoPE and the casts applied
  * to those bf16 values are bit-identical.
@@ -108,7 +109,18 @@ int gllm_qkv_rope_kv_write(const void* x, int64_t x_row_stride, int64_t num_toke
                            int64_t num_slots, const int64_t* slot_mapping, const int32_t* query_lens,
                            int64_t tokens_per_seq, const void* cos, const void* sin, const int64_t* rope_rows,
                            int64_t rope_row_stride, int32_t num_q_heads, int32_t num_kv_heads,
-                           int32_t head_dim, int32_t dtype, int32_t kv_dtype, void* stream);
+                           int32_t head_dim, int32_t dtype, int32_t kv_dtype, void* workspace,
+                           size_t workspace_bytes, void* stream);
+/* Device bytes gllm_qkv_rope_kv_write can use as `workspace` for this batch
+ * (0: none).  With a workspace of at least that size, batches too small to
+ * fill the GPU with (128-token x head) tiles (decode) split the hidden
+ * dimension over more workgroups: fp32 partial sums go to the workspace and
+ * a second small launch sums them in fixed order (deterministic) before the
+ * RoPE and the stores.  Without it the tile kernel runs (same results up to
+ * the fp32 summation order of the projections).  No library counterpart in
+ * the reference: F.linear needs none. */
+size_t gllm_qkv_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t num_q_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int32_t with_q);
 
 /*
  * Rotate k (and, if q_out != NULL, q) with rotate-half RoPE and write k/v rows

@@ -144,3 +144,61 @@ def test_qkv_rejects_bad_arguments():
     w32 = torch.zeros(128, 128, dtype=torch.float32, device=DEV)
     with pytest.raises(NotImplementedError):
         paged.qkv_rope_kv_write(x32, None, w32, w32, cs.float(), cs.float(), kc.float(), kc.float().clone(), sl)
+
+
+@pytest.mark.parametrize("n,hidden,Hq,Hkv,D", [(64, 2048, 32, 8, 64), (70, 1024, 8, 2, 128), (3, 4096, 32, 8, 128)])
+def test_qkv_split_k_exact_and_matches_tile_path(n, hidden, Hq, Hkv, D):
+    """Few tokens: the hidden dimension is split over workgroups (fp32
+    partials summed in fixed order by a second launch).  Sparse small
+    integers keep every partial and total exact, so q / K / V are bit-exact
+    against the oracle and against the tile kernel (split_k=False)."""
+    print(f"qkv split-k n={n} hidden={hidden} Hq={Hq} Hkv={Hkv} D={D}", flush=True)
+    from gllm_amd import _lib
+    lib = _lib.load()
+    assert lib.gllm_qkv_workspace_bytes(n, hidden, Hq, Hkv, D, 1) > 0      # the split path is planned
+    g = torch.Generator().manual_seed(40 + n)
+
+    def sparse(*shape):
+        v = torch.randint(-1, 2, shape, generator=g)
+        return (v * (torch.rand(shape, generator=g) < 0.15)).to(BF)
+
+    x = sparse(n, hidden)
+    wq, wk, wv = sparse(Hq * D, hidden), sparse(Hkv * D, hidden), sparse(Hkv * D, hidden)
+    cos_t, sin_t = orope.rope_cache(4096, D, 500000.0, BF)
+    pos = torch.randint(0, 4096, (n,), generator=g)
+    ns = 2 * n + 16
+    slots = torch.randperm(ns, generator=g)[:n].to(torch.int64)
+    outs = []
+    for split in (True, False):
+        kc = torch.full((ns, Hkv, D), 3.0, dtype=BF, device=DEV)
+        vc = kc.clone()
+        q = paged.qkv_rope_kv_write(x.to(DEV), wq.to(DEV), wk.to(DEV), wv.to(DEV), cos_t.to(DEV), sin_t.to(DEV),
+                                    kc, vc, slots.to(DEV), rope_rows=pos.to(DEV), split_k=split)
+        torch.cuda.synchronize()
+        outs.append((q.cpu(), kc.cpu(), vc.cpu()))
+    kr = torch.full((ns, Hkv, D), 3.0, dtype=BF)
+    vr = kr.clone()
+    qr = op.qkv_rope_kv_write(x, wq, wk, wv, cos_t[pos], sin_t[pos], kr, vr, slots, Hkv, D)
+    for q, kc, vc in outs:
+        assert torch.equal(q.view(torch.int16), qr.view(torch.int16))
+        assert torch.equal(kc.view(torch.int16), kr.view(torch.int16))
+        assert torch.equal(vc.view(torch.int16), vr.view(torch.int16))
+
+
+def test_qkv_split_k_random_matches_tile_path():
+    """N(0,1) data: split and tile paths differ only by the fp32 summation
+    order of the projections (at most one bf16 ulp before RoPE)."""
+    print("qkv split-k vs tile, random", flush=True)
+    n, hidden, Hq, Hkv, D = 64, 2048, 32, 8, 64
+    x, (wq, wk, wv), cos_t, sin_t, pos, slots, ns = _inputs(n, hidden, Hq, Hkv, D, False, 77)
+    res = []
+    for split in (True, False):
+        kc = torch.zeros(ns, Hkv, D, dtype=BF, device=DEV)
+        vc = torch.zeros_like(kc)
+        q = paged.qkv_rope_kv_write(x.to(DEV), wq.to(DEV), wk.to(DEV), wv.to(DEV), cos_t.to(DEV), sin_t.to(DEV),
+                                    kc, vc, slots.to(DEV), rope_rows=pos.to(DEV), split_k=split)
+        torch.cuda.synchronize()
+        res.append((q.cpu(), kc.cpu()[slots], vc.cpu()[slots]))
+    _close_bf16(res[0][0], res[1][0], "q", True)
+    _close_bf16(res[0][1], res[1][1], "k", True)
+    _close_bf16(res[0][2], res[1][2], "v", False)
