@@ -77,19 +77,26 @@ __device__ __forceinline__ f32x4 mfma16k16(u32x2 a, u32x2 b, f32x4 c) {
 // the kv head are the 16 MFMA columns.  The KW waves of a head merge through
 // LDS; a split sequence writes (max, sum, acc) partials that merge_splits
 // combines in a second, tiny launch (no cross-workgroup fences here).
-// One lane's 8 cached elements: 16 bytes of bf16, or 8 bytes of fp8 that are
-// widened (exactly) to bf16 on use.
-template <bool KV8> struct KVChunk;
-template <> struct KVChunk<false> {
-  typedef u32x4 T;
-  __device__ static T load(const char* p) { return ld16(p); }
-  __device__ static u32x4 bf16(T x) { return x; }
-};
-template <> struct KVChunk<true> {
-  typedef u32x2 T;
-  __device__ static T load(const char* p) { return *reinterpret_cast<const u32x2*>(p); }
-  __device__ static u32x4 bf16(T x) { return fp8x8_to_bf16x8(x[0], x[1]); }
-};
+// Cached K/V come in 16-byte loads per lane: 8 bf16 dims, or 16 fp8 dims
+// that are widened (exactly) to bf16 on use and feed two MFMA K-chunks.
+// Head dim of element i of MFMA chunk kk in lane group grp:
+//   bf16: 32 kk + 8 grp + i
+//   fp8:  64 (kk / 2) + 16 grp + 8 (kk % 2) + i
+// S = K Q^T sums over dims, so any order serves as long as K and Q agree;
+// V is staged to LDS in natural dim order, so the output is too.
+template <bool KV8>
+__device__ __forceinline__ int chunk_dim(int kk, int grp) {
+  return KV8 ? 64 * (kk >> 1) + 16 * grp + 8 * (kk & 1) : 32 * kk + 8 * grp;
+}
+template <bool KV8>
+__device__ __forceinline__ u32x4 chunk_bf16(const u32x4* raw, int kk) {
+  if constexpr (KV8) {
+    const u32x4 w = raw[kk >> 1];
+    return (kk & 1) ? fp8x8_to_bf16x8(w[2], w[3]) : fp8x8_to_bf16x8(w[0], w[1]);
+  } else {
+    return raw[kk];
+  }
+}
 
 // One decode task: keys [kbeg, kend) of one sequence for HW kv heads.
 struct DecodeTask {
@@ -106,11 +113,15 @@ template <int D, int HW, int KW, bool KV8>
 __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask& tk, char* lds, int* ticket_lds) {
   constexpr int NW = HW * KW;
   constexpr int E = KV8 ? 1 : 2;   // bytes per cached element
-  using KC = KVChunk<KV8>;
   using Cfg = DecodeCfg<D, NW>;
   constexpr int NK = D / 32;   // 32-dim K chunks per key
+  constexpr int NL = KV8 ? NK / 2 : NK;   // 16-byte loads per key (K and V each)
   constexpr int ND = D / 16;   // 16-dim output blocks
   constexpr int RB = Cfg::kRowBytes;
+  // RoPE partners d, d + D/2 in the same lane (chunks kk, kk + NK/2), except
+  // for fp8 at D = 64, where a lane's 16 dims lie in one half
+  constexpr bool kPairInLane = !KV8 || D >= 128;
+  constexpr int NC = kPairInLane ? NK / 2 : NK;   // cos/sin loads
   constexpr int PF = Cfg::kPF;
   // the thread id through an opaque move: nothing derived from it is hoisted
   // out of a caller's loop over tasks (which would hold it in registers
@@ -145,36 +156,59 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
   const int nblk = ((kend - 1) >> a.block_shift) - blk0 + 1;
   const int32_t* bt = a.block_table + (int64_t)seq * a.block_table_stride + blk0;
   const uint32_t bid = tid < nblk ? (uint32_t)bt[tid] : 0u;
-  const __bf16* qp = (const __bf16*)a.q + qrow * a.q_row_stride + (int64_t)qh * D + 8 * grp;
-  u32x4 qraw[NK], craw[NK / 2], sraw[NK / 2];
+  const __bf16* qp = (const __bf16*)a.q + qrow * a.q_row_stride + (int64_t)qh * D;
+  u32x4 qraw[NK], praw[kPairInLane ? 1 : NK], craw[NC], sraw[NC];
 #pragma unroll
-  for (int kk = 0; kk < NK; ++kk) qraw[kk] = ld16(qp + 32 * kk);
+  for (int kk = 0; kk < NK; ++kk) qraw[kk] = ld16(qp + chunk_dim<KV8>(kk, grp));
   const bool rope = a.rope_mode != kRopeNone;
   if (rope) {
     const int64_t crow = a.rope_mode == kRopeByPosition ? (int64_t)vis : qrow;
-    const __bf16* cp = (const __bf16*)a.rope_cos + crow * a.rope_row_stride + 8 * grp;
-    const __bf16* sp = (const __bf16*)a.rope_sin + crow * a.rope_row_stride + 8 * grp;
+    const __bf16* cp = (const __bf16*)a.rope_cos + crow * a.rope_row_stride;
+    const __bf16* sp = (const __bf16*)a.rope_sin + crow * a.rope_row_stride;
 #pragma unroll
-    for (int kk = 0; kk < NK / 2; ++kk) {
-      craw[kk] = ld16(cp + 32 * kk);
-      sraw[kk] = ld16(sp + 32 * kk);
+    for (int kk = 0; kk < NC; ++kk) {
+      const int d = chunk_dim<KV8>(kk, grp) & (D / 2 - 1);
+      craw[kk] = ld16(cp + d);
+      sraw[kk] = ld16(sp + d);
+    }
+    if constexpr (!kPairInLane) {
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) praw[kk] = ld16(qp + (chunk_dim<KV8>(kk, grp) ^ (D / 2)));
     }
   }
   if (tid < nblk) lbid[tid] = bid < (uint64_t)a.num_blocks ? (int32_t)bid : 0;  // never address outside the pool
 
-  // Q as the B operand of S^T = K Q^T: lane holds Q[row n][32kk + 8grp + i].
+  // Q as the B operand of S^T = K Q^T: lane holds Q[row n][chunk_dim(kk) + i].
   bf16x8 qB[NK];
   {
     float x[NK][8];
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) unpack_bf16x8(qraw[kk], x[kk]);
     if (rope) {
+      if constexpr (kPairInLane) {
 #pragma unroll
-      for (int kk = 0; kk < NK / 2; ++kk) {
-        float c[8], s[8];
-        unpack_bf16x8(craw[kk], c);
-        unpack_bf16x8(sraw[kk], s);
-        rope8_bf16(x[kk], x[kk + NK / 2], c, s);
+        for (int kk = 0; kk < NK / 2; ++kk) {
+          float c[8], s[8];
+          unpack_bf16x8(craw[kk], c);
+          unpack_bf16x8(sraw[kk], s);
+          rope8_bf16(x[kk], x[kk + NK / 2], c, s);
+        }
+      } else {
+        // the same roundings as rope8_bf16, one half of the pair per lane
+        const bool first = chunk_dim<KV8>(0, grp) < D / 2;
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk) {
+          float c[8], s[8], xp[8];
+          unpack_bf16x8(craw[kk], c);
+          unpack_bf16x8(sraw[kk], s);
+          unpack_bf16x8(praw[kk], xp);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float u = round_bf16(__fmul_rn(x[kk][i], c[i]));
+            const float v = round_bf16(__fmul_rn(xp[i], s[i]));
+            x[kk][i] = round_bf16(first ? __fsub_rn(u, v) : __fadd_rn(u, v));
+          }
+        }
       }
     }
 #pragma unroll
@@ -188,8 +222,8 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
 
   // byte addressing: slot (< 2^32) x slot bytes (< 2^32) is one 32x32->64 mad
   const uint32_t sbytes = (uint32_t)(a.cache_slot_stride * E);
-  const char* kc = (const char*)a.k_cache + ((int64_t)(head_ok ? kvh : 0) * D + 8 * grp) * E;
-  const char* vc = (const char*)a.v_cache + ((int64_t)(head_ok ? kvh : 0) * D + 8 * grp) * E;
+  const char* kc = (const char*)a.k_cache + (int64_t)(head_ok ? kvh : 0) * D * E + 16 * grp;
+  const char* vc = (const char*)a.v_cache + (int64_t)(head_ok ? kvh : 0) * D * E + 16 * grp;
   const float sl2 = a.scale * kLog2e;
   char* ldsV = lds + wave * Cfg::kVBytes;
   const uint32_t bmask = a.block_size - 1;
@@ -201,28 +235,28 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
 
   // this wave's sub-tiles: j = ki + KW * t, t < ntw
   const int ntw = head_ok && nsub > ki ? (nsub - ki + KW - 1) / KW : 0;
-  typename KC::T kr[PF + 1][NK], vr[PF + 1][NK];
-  auto issue = [&](int t, typename KC::T (&kd)[NK], typename KC::T (&vd)[NK]) {
+  u32x4 kr[PF + 1][NL], vr[PF + 1][NL];
+  auto issue = [&](int t, u32x4 (&kd)[NL], u32x4 (&vd)[NL]) {
     // ring padding (t >= ntw): every lane reads the task's last slot, one
     // cache line per load instead of a whole 16-key tile
     const int key = t < ntw ? min(kbeg + 16 * (ki + KW * t) + n, kend - 1) : kend - 1;
     const uint32_t slot = (uint32_t)lbid[(key >> a.block_shift) - blk0] * (uint32_t)a.block_size + ((uint32_t)key & bmask);
     const uint64_t off = (uint64_t)slot * sbytes;
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) {
-      kd[kk] = KC::load(kc + off + 32 * E * kk);
-      vd[kk] = KC::load(vc + off + 32 * E * kk);
+    for (int l = 0; l < NL; ++l) {
+      kd[l] = ld16(kc + off + 64 * l);
+      vd[l] = ld16(vc + off + 64 * l);
     }
   };
-  auto compute = [&](int t, const typename KC::T (&kd)[NK], const typename KC::T (&vd)[NK]) {
+  auto compute = [&](int t, const u32x4 (&kd)[NL], const u32x4 (&vd)[NL]) {
     // tiles past the last one (ring padding) are fully masked
     const int kb = t < ntw ? kbeg + 16 * (ki + KW * t) : kend;
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) s = mfma16(as_bf16x8(KC::bf16(kd[kk])), qB[kk], s);
+    for (int kk = 0; kk < NK; ++kk) s = mfma16(as_bf16x8(chunk_bf16<KV8>(kd, kk)), qB[kk], s);
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk)
-      *reinterpret_cast<u32x4*>(ldsV + n * RB + (32 * kk + 8 * grp) * 2) = KC::bf16(vd[kk]);
+      *reinterpret_cast<u32x4*>(ldsV + n * RB + chunk_dim<KV8>(kk, grp) * 2) = chunk_bf16<KV8>(vd, kk);
     // lane holds S[key kb + 4grp + j][row n]
     float p[4];
 #pragma unroll
@@ -948,12 +982,28 @@ template <int D, bool PF, bool DC, int NW> struct MixedLds {
   static constexpr int kBytes = a > b ? a : b;
 };
 
+// Workgroup b of a launch is dispatched to XCD b % 8, and each XCD has its
+// own L2.  When a decode workgroup reads less than a 128-byte line of each
+// slot (fp8 cache, HW x D < 128 bytes), the neighbouring kv-head group reads
+// the rest of the line; unless both run on one XCD, both L2s fetch the whole
+// line from HBM.  Grouped, every 64 workgroups are transposed (8 x 8) so
+// that XCD x runs items 8x .. 8x+7 of the 64, i.e. the consecutive head
+// groups of one sequence (a ragged last group keeps its order).  The
+// planner's pairing of item k with item k + CUs on one CU survives: the same
+// transposition applies to every full 64.
+template <bool GROUP>
+__device__ __forceinline__ int xcd_item(int b, int n) {
+  if (!GROUP || (b | 63) >= n) return b;
+  const int P = b & 63;
+  return (b & ~63) + (P & 7) * 8 + (P >> 3);
+}
+
 // Work items of both kinds in one launch (mixed continuous batch; 8-wave
 // workgroups), or decode items only (HW x KW waves).
 template <int D, bool PF, bool DC, int HW, int KW, bool KV8>
 __global__ void __launch_bounds__(64 * HW * KW) paged_attn_bf16_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[MixedLds<D, PF, DC, HW * KW>::kBytes];
-  const WorkItem it = a.items[blockIdx.x];
+  const WorkItem it = a.items[xcd_item<!PF && KV8 && HW * D < 128>(blockIdx.x, a.n_items)];
   if (PF && (!DC || (it.kind_b & 0xff) == kItemPrefill)) {
     if constexpr (HW * KW == kWaves)
       prefill_wg<D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);

@@ -115,3 +115,27 @@ def test_fp8_widening_exact(D):
     # exact values (the accumulator starts at +0, so code 0x80 = -0.0 comes back as +0.0)
     got, want = out.cpu().float(), rows.to(torch.bfloat16).float()
     assert torch.equal(got, want), (got - want).abs().max().item()
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("split", [0, paged.BALANCED])
+@pytest.mark.parametrize("kv8", [False, True])
+def test_decode_rope_in_kernel_bit_exact(D, split, kv8):
+    """Decode with q rotated in the kernel's prologue returns exactly what the
+    same kernel returns for q rotated first by the reference's apply_rope
+    (gllm/model/layers/attention.py:105-118, the oracle's restatement): the
+    in-register rotation must round like torch's bf16 ops, element for
+    element.  An fp8 lane at D = 64 holds one half of each rotate pair and
+    loads the other half as well, so that case has its own code."""
+    print(f"decode rope fused exact D={D} split={split} kv8={kv8}", flush=True)
+    b = make_batch([10, 500, 1999, 63], [1, 1, 1, 1], 32, 8, D, theta=500000.0)
+    if kv8:
+        b = _fp8(b)
+    pos = torch.tensor(b.ctx_lens)
+    q_rot = orope.apply_rope(b.q.cpu().unsqueeze(0), b.cos.cpu()[pos].unsqueeze(0), b.sin.cpu()[pos].unsqueeze(0))[0]
+    plan = _plan(b, split_tokens=split)
+    fused = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table, rope=(b.cos, b.sin, "position"))
+    pre = paged.paged_attention(plan, q_rot.to(DEV), b.k_cache, b.v_cache, b.block_table)
+    torch.cuda.synchronize()
+    assert torch.equal(fused.cpu(), pre.cpu()), (fused.float() - pre.float()).abs().max().item()
+    assert_close_bf16(fused, oracle_paged(b, q_rot), "decode fused rope")
