@@ -315,6 +315,13 @@ def main():
         extra["metadata_mixed_8b"] = bench_metadata(xd, args.warmup, args.steps, dev, False)
         del xd
         torch.cuda.empty_cache()
+        # the decode sequences of the same batch alone: decode at the 8B head shape
+        d = workloads.config_d()
+        dd = workloads.PagedBatch("decode_8b", d.ctx_lens[:256], d.q_lens[:256], d.num_q_heads, d.num_kv_heads,
+                                  d.head_dim, d.block_size, d.num_blocks, d.dtype, rope_theta=d.rope_theta)
+        r, _, _ = bench_decode(dd, 1, args.warmup, args.steps, args.split, dev, args.hw)
+        extra["decode_8b"] = r
+        torch.cuda.empty_cache()
     if "e" in cfgs:
         r, _, _ = bench_decode(workloads.config_e(), 1, args.warmup, max(5, args.steps // 3), args.split, dev, args.hw)
         extra["long_decode_70b"] = r
