@@ -71,6 +71,31 @@ def test_config_b_decode_full():
         assert (o - outs[0]).abs().max().item() < 2e-2
 
 
+def test_config_b_decode_full_fp8():
+    """Config (b) over an fp8 (e4m3fn) pool: 512 decode workgroups of one kv
+    head each, which the kernel regroups by XCD in blocks of 64 (eight full
+    blocks here: a mapping that ran an item twice and another never would
+    leave rows unwritten); every row against the fp32 oracle on the same fp8
+    cache, and the result independent of the workgroup shape."""
+    print("config b full fp8", flush=True)
+    cb = workloads.config_b()
+    cb.kv_dtype = torch.float8_e4m3fn
+    b = workloads.materialize(cb, DEV, values_on_device=True)
+    assert b.k_cache.dtype == torch.float8_e4m3fn
+    ref = _oracle_rows(b, [(i, 0) for i in range(len(b.q_lens))], b.q.cpu())
+    outs = []
+    for hw, split in ((0, 0), (1, 0), (2, 0), (8, 128), (0, paged.BALANCED)):
+        plan = _plan(b, heads_per_wg=hw, split_tokens=split)
+        if hw == 0 and split == 0:
+            assert plan.info["heads_per_wg"] == 1 and plan.info["work_items"] == 512
+        out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
+        torch.cuda.synchronize()
+        assert_close_bf16(out, ref, f"config b fp8 hw={hw} split={split}")
+        outs.append(out.float().cpu())
+    for o in outs[1:]:
+        assert (o - outs[0]).abs().max().item() < 2e-2
+
+
 def test_config_c_prefill_full():
     print("config c full", flush=True)
     b = workloads.materialize(workloads.config_c(), DEV, values_on_device=True)
