@@ -10,11 +10,14 @@
 // k and v cast to the cache dtype and stored at slot_mapping[token]
 // (attention.py:156-161), padded rows skipped; q written to q_out.
 //
-// Tiling: one 4-wave workgroup per (128 tokens, one head of D outputs).
-// X and W K-slices of 32 stream HBM/L2 -> LDS with global_load_lds into a
-// 4-stage ring (XOR-swizzled 16-byte chunks: operand reads are bank-conflict
-// free); each wave computes 32 tokens x D outputs on v_mfma_f32_32x32x16_bf16
-// (D/32 accumulator blocks).  Output column n of block b is head dim
+// Tiling: one 4-wave workgroup per (128 tokens, one head of D outputs); for
+// large batches at D = 128, one 8-wave workgroup per (256 tokens, two heads)
+// whose waves each take 64 tokens x one head (two row blocks share every W
+// operand read), launched in XCD-grouped order (qkv_groups).  X and W
+// K-slices of 32 stream HBM/L2 -> LDS with global_load_lds into a 4-stage
+// ring (XOR-swizzled 16-byte chunks: operand reads are bank-conflict free);
+// each wave computes 32 tokens x D outputs per row block on
+// v_mfma_f32_32x32x16_bf16 (D/32 accumulator blocks).  Output column n of block b is head dim
 // 32b + n, so a RoPE pair (d, d + D/2) sits in blocks b and b + D/64 of the
 // same lane: the rotation happens in registers and every value is stored
 // from its lane (2-byte stores, 64-byte runs per half-wave).  Batches too
@@ -39,6 +42,27 @@ __device__ __forceinline__ void rope1_bf16(float& x1, float& x2, float c, float 
   x2 = round_bf16(__fadd_rn(e, f));
 }
 
+// XCD-grouped order of the large-batch tiles: workgroup b of the launch runs
+// on XCD b % kXcds, and each XCD takes super-groups of gt token tiles x gh
+// head groups (gt * gh = the workgroups one XCD holds at once), so the
+// workgroups of a super-group stream the same X and W K-slices through that
+// XCD's L2 together.  gh divides the head-group count where it can, so no
+// slot of a super-group idles.
+constexpr int kXcds = 8;
+struct QKVGroups { int gt, gh, nhg; int64_t nsg; };
+__host__ __device__ inline QKVGroups qkv_groups(int64_t tiles, int ngroups, int cus) {
+  const int slots = cus / kXcds > 0 ? cus / kXcds : 1;
+  int gh = 1;
+  for (int c = 8; c > 1; c >>= 1)
+    if (c <= slots && ngroups % c == 0) { gh = c; break; }
+  QKVGroups g;
+  g.gh = gh;
+  g.gt = slots / gh > 0 ? slots / gh : 1;
+  g.nhg = (ngroups + gh - 1) / gh;
+  g.nsg = ((tiles + g.gt - 1) / g.gt) * g.nhg;
+  return g;
+}
+
 // Physical 16-byte chunk of logical chunk c in 64-byte LDS row r: rows
 // r, r+4, r+8, r+12 get the 4 chunk rotations, so 16 consecutive rows
 // reading one logical chunk hit 16 distinct bank groups.
@@ -46,31 +70,52 @@ __device__ __forceinline__ int qkv_swz(int r) { return (r >> 2) & 3; }
 
 }  // namespace
 
-template <int D, bool KV8>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) qkv_rope_write_kernel(QKVArgs a) {
-  constexpr int TM = 128;                 // tokens per workgroup
+// TM tokens x HP heads per workgroup; each wave computes 32 RB tokens x one
+// head (RB row blocks share every W operand read).
+template <int D, bool KV8, int TM, int RB = 1, int HP = 1, bool GROUPED = false>
+__global__ void __launch_bounds__(64 * (TM / (32 * RB)) * HP) __attribute__((amdgpu_waves_per_eu(2)))
+qkv_rope_write_kernel(QKVArgs a) {
+  constexpr int TG = TM / (32 * RB);      // token groups (waves per head)
+  constexpr int NT = 64 * TG * HP;        // threads
   constexpr int BK = 32;                  // K slice per stage
   constexpr int NS = 4;                   // LDS ring stages
-  constexpr int NB = D / 32;              // accumulator blocks per wave (32 x 32 each)
+  constexpr int NB = D / 32;              // accumulator blocks per row block (32 x 32 each)
   constexpr int ROWB = BK * 2;            // 64-byte LDS rows
   constexpr int A_BYTES = TM * ROWB;      // X slice
-  constexpr int B_BYTES = D * ROWB;       // W slice
+  constexpr int B_BYTES = HP * D * ROWB;  // W slice (HP heads of one kind, consecutive W rows)
   constexpr int STAGE = A_BYTES + B_BYTES;
-  constexpr int IA = A_BYTES / (256 * 16);          // copy instructions per thread per stage: X
-  constexpr int IB = B_BYTES / (256 * 16);          //                                          W
+  constexpr int IA = A_BYTES / (NT * 16);           // copy instructions per thread per stage: X
+  constexpr int IB = B_BYTES / (NT * 16);           //                                          W
   constexpr int IPS = IA + IB;
-  static_assert(IA >= 1 && IB >= 1 && A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "tile / workgroup mismatch");
+  static_assert(IA >= 1 && IB >= 1 && A_BYTES % (NT * 16) == 0 && B_BYTES % (NT * 16) == 0, "tile / workgroup mismatch");
   __shared__ __attribute__((aligned(16))) char lds[NS * STAGE];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int head = blockIdx.y;
-  const int kind = head < a.num_q_heads ? 0 : (head < a.num_q_heads + a.num_kv_heads ? 1 : 2);   // q, k, v
-  const int h = kind == 0 ? head : (kind == 1 ? head - a.num_q_heads : head - a.num_q_heads - a.num_kv_heads);
-  const char* w = (const char*)(kind == 0 ? a.w_q : (kind == 1 ? a.w_k : a.w_v));
-  const int64_t wstride = kind == 0 ? a.w_q_row_stride : (kind == 1 ? a.w_k_row_stride : a.w_v_row_stride);
-  w += (int64_t)h * D * wstride * 2;
   const int64_t N = a.num_tokens;
-  const int64_t tok0 = (int64_t)blockIdx.x * TM;
+  int head, tile;
+  if constexpr (GROUPED) {
+    // 1-D grid in XCD-grouped order (qkv_groups)
+    const int ngroups = (a.num_q_heads + 2 * a.num_kv_heads) / HP;
+    const QKVGroups gr = qkv_groups((N + TM - 1) / TM, ngroups, a.cus);
+    const int S = gr.gt * gr.gh;
+    const int b = blockIdx.x, xcd = b % kXcds, j = b / kXcds;
+    const int sg = xcd + kXcds * (j / S), wi = j % S;
+    tile = (sg / gr.nhg) * gr.gt + wi / gr.gh;
+    head = (sg % gr.nhg) * gr.gh + wi % gr.gh;
+    if ((int64_t)tile * TM >= N || head >= ngroups) return;   // padding of the last super-groups
+  } else {
+    head = blockIdx.y;
+    tile = blockIdx.x;
+  }
+  head *= HP;                             // first head of the workgroup (all HP of one kind)
+  const int kind0 = head < a.num_q_heads ? 0 : (head < a.num_q_heads + a.num_kv_heads ? 1 : 2);   // q, k, v
+  const int h0 = kind0 == 0 ? head : (kind0 == 1 ? head - a.num_q_heads : head - a.num_q_heads - a.num_kv_heads);
+  const char* w = (const char*)(kind0 == 0 ? a.w_q : (kind0 == 1 ? a.w_k : a.w_v));
+  const int64_t wstride = kind0 == 0 ? a.w_q_row_stride : (kind0 == 1 ? a.w_k_row_stride : a.w_v_row_stride);
+  w += (int64_t)h0 * D * wstride * 2;
+  const int64_t tok0 = (int64_t)tile * TM;
+  const int kind = kind0, h = h0 + wave / TG;   // this wave's head
+  const int tg = wave % TG;                      // this wave's token group
   const int nk = a.hidden / BK;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
 
@@ -82,7 +127,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) q
 #pragma unroll
     for (int i = 0; i < IPS; ++i) {
       const bool isA = i < IA;
-      const int c = (isA ? i : i - IA) * 256 + tid;
+      const int c = (isA ? i : i - IA) * NT + tid;
       const int row = c >> 2, lc = (c & 3) ^ qkv_swz(row);
       const char* src;
       if (isA) {
@@ -92,18 +137,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) q
         src = w + (int64_t)row * wstride * 2 + k0b + lc * 16;
       }
       const uint32_t dst = __builtin_amdgcn_readfirstlane(
-          lds0 + stage * STAGE + (isA ? 0 : A_BYTES) + ((isA ? i : i - IA) * 256 + wave * 64) * 16);
+          lds0 + stage * STAGE + (isA ? 0 : A_BYTES) + ((isA ? i : i - IA) * NT + wave * 64) * 16);
       lds_dma16(src, dst);
     }
   };
 
-  f32x16 acc[NB];
+  f32x16 acc[RB][NB];
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
+  for (int r = 0; r < RB; ++r)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) acc[b][j] = 0.f;
-  const bool wact = tok0 + wave * 32 < N;     // this wave's 32 tokens hold at least one real one
-  const int ar = wave * 32 + (lane & 31);     // X row of the A operand
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[r][b][j] = 0.f;
+  const bool wact = tok0 + tg * 32 * RB < N;  // this wave's tokens hold at least one real one
+  const int ar = tg * 32 * RB + (lane & 31);  // X row of the A operand (+ 32 r)
+  const int bh = (wave / TG) * D;             // first W row of this wave's head in the tile
   const int hi = lane >> 5;
 
 #pragma unroll
@@ -127,12 +175,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) q
 #pragma unroll
       for (int kk = 0; kk < BK / 16; ++kk) {
         const int lc = 2 * kk + hi;
-        const bf16x8 av = __builtin_bit_cast(bf16x8, ld16(As + ar * ROWB + ((lc ^ qkv_swz(ar)) << 4)));
+        bf16x8 av[RB];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+          const int arr = ar + 32 * r;
+          av[r] = __builtin_bit_cast(bf16x8, ld16(As + arr * ROWB + ((lc ^ qkv_swz(arr)) << 4)));
+        }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-          const int br = 32 * b + (lane & 31);
+          const int br = bh + 32 * b + (lane & 31);
           const bf16x8 bv = __builtin_bit_cast(bf16x8, ld16(Bs + br * ROWB + ((lc ^ qkv_swz(br)) << 4)));
-          acc[b] = mfma32(av, bv, acc[b]);
+#pragma unroll
+          for (int r = 0; r < RB; ++r) acc[r][b] = mfma32(av[r], bv, acc[r][b]);
         }
       }
     }
@@ -146,7 +200,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) q
   const int n = lane & 31;
   const bool rope = kind == 1 || (kind == 0 && a.rotate_q);
   constexpr int NH = NB / 2;
-  const int64_t tbase = tok0 + wave * 32 + 4 * hi;
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+  const int64_t tbase = tok0 + tg * 32 * RB + 32 * r + 4 * hi;
   int64_t dst[16];            // store offset per token (elements), -1: not written
   uint32_t csn[16][NH];       // cos (low 16 bits) and sin (high) of the lane's rotation pairs
   {
@@ -205,7 +261,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) q
   for (int j = 0; j < 16; ++j) {
     float v[NB];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) v[b] = round_bf16(acc[b][j]);     // F.linear's bf16 output
+    for (int b = 0; b < NB; ++b) v[b] = round_bf16(acc[r][b][j]);  // F.linear's bf16 output
     if (rope) {
 #pragma unroll
       for (int b = 0; b < NH; ++b)
@@ -223,6 +279,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) q
       for (int b = 0; b < NB; ++b)
         *reinterpret_cast<uint16_t*>(cp + (32 * b + n) * 2) = (uint16_t)pack_bf16x2(v[b], 0.f);
     }
+  }
   }
 }
 
@@ -434,11 +491,24 @@ hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t st) {
   }
   const dim3 grid((unsigned)tiles, (unsigned)heads), block(256);
   if (a.head_dim == 64) {
-    if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<64, true>), grid, block, 0, st, b);
-    else hipLaunchKernelGGL((qkv_rope_write_kernel<64, false>), grid, block, 0, st, b);
+    if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<64, true, 128>), grid, block, 0, st, b);
+    else hipLaunchKernelGGL((qkv_rope_write_kernel<64, false, 128>), grid, block, 0, st, b);
   } else if (a.head_dim == 128) {
-    if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<128, true>), grid, block, 0, st, b);
-    else hipLaunchKernelGGL((qkv_rope_write_kernel<128, false>), grid, block, 0, st, b);
+    // Large batches: 256 tokens x 2 heads per 8-wave workgroup (each wave 64
+    // tokens x one head: two row blocks share every W operand read), in
+    // XCD-grouped order; they need heads that pair within q and within k/v.
+    const int64_t tiles2 = (a.num_tokens + 255) / 256;
+    if (b.num_q_heads % 2 == 0 && a.num_kv_heads % 2 == 0 && tiles2 * (heads / 2) >= 2 * (int64_t)a.cus) {
+      const QKVGroups gr = qkv_groups(tiles2, heads / 2, a.cus);
+      const int64_t wgs = (int64_t)kXcds * gr.gt * gr.gh * ((gr.nsg + kXcds - 1) / kXcds);
+      if (wgs > 0x7fffffff) return hipErrorInvalidValue;
+      const dim3 grid2((unsigned)wgs), block2(512);
+      if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<128, true, 256, 2, 2, true>), grid2, block2, 0, st, b);
+      else hipLaunchKernelGGL((qkv_rope_write_kernel<128, false, 256, 2, 2, true>), grid2, block2, 0, st, b);
+      return hipGetLastError();
+    }
+    if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<128, true, 128>), grid, block, 0, st, b);
+    else hipLaunchKernelGGL((qkv_rope_write_kernel<128, false, 128>), grid, block, 0, st, b);
   } else {
     return hipErrorInvalidValue;
   }

@@ -72,7 +72,10 @@ def _run(n, hidden, Hq, Hkv, D, integer, seed, kv_dtype=BF, rotate_q=True, with_
 
 
 @pytest.mark.parametrize("n,hidden,Hq,Hkv,D", [(1, 128, 4, 2, 64), (130, 128, 8, 2, 128), (300, 256, 16, 4, 64),
-                                               (77, 96, 4, 4, 128)])
+                                               (77, 96, 4, 4, 128),
+                                               # prefill-sized batches, ragged last tile: 128-token
+                                               # tiles, then 256-token x 2-head tiles in XCD order
+                                               (2300, 128, 8, 2, 128), (6000, 64, 32, 8, 128)])
 def test_qkv_exact_on_integer_data(n, hidden, Hq, Hkv, D):
     """Exact GEMM (small integers): q, the cached k (rotated) and v bit-exact,
     untouched slots keep their sentinel."""
@@ -84,7 +87,8 @@ def test_qkv_exact_on_integer_data(n, hidden, Hq, Hkv, D):
 
 
 @pytest.mark.parametrize("n,hidden,Hq,Hkv,D", [(64, 2048, 32, 8, 64), (259, 4096, 32, 8, 128),
-                                               (131, 1024, 8, 1, 128), (5, 512, 16, 16, 64)])
+                                               (131, 1024, 8, 1, 128), (5, 512, 16, 16, 64),
+                                               (2085, 1024, 8, 2, 128), (5500, 256, 32, 8, 128)])
 def test_qkv_random_data(n, hidden, Hq, Hkv, D):
     """Llama-shaped projections (1B: hidden 2048 / D 64; 8B: 4096 / 128) on
     N(0,1) data: within the GEMM's accumulation-order rounding."""
@@ -104,10 +108,11 @@ def test_qkv_unrotated_q_and_fp8_cache():
     values (exact data, so byte-exact)."""
     print("qkv unrotated q, fp8 cache", flush=True)
     f8 = torch.float8_e4m3fn
-    q, qr, kc, vc, kr, vr, slots, ns = _run(90, 128, 8, 2, 64, True, 21, kv_dtype=f8, rotate_q=False)
-    assert torch.equal(q.cpu().view(torch.int16), qr.view(torch.int16))
-    assert torch.equal(kc.view(torch.uint8), kr.view(torch.uint8))
-    assert torch.equal(vc.view(torch.uint8), vr.view(torch.uint8))
+    for n, hidden, Hq, Hkv, D in ((90, 128, 8, 2, 64), (6000, 64, 32, 8, 128)):   # small and large-batch tiles
+        q, qr, kc, vc, kr, vr, slots, ns = _run(n, hidden, Hq, Hkv, D, True, 21, kv_dtype=f8, rotate_q=False)
+        assert torch.equal(q.cpu().view(torch.int16), qr.view(torch.int16))
+        assert torch.equal(kc.view(torch.uint8), kr.view(torch.uint8))
+        assert torch.equal(vc.view(torch.uint8), vr.view(torch.uint8))
 
 
 def test_qkv_without_q_and_padded_rows():
