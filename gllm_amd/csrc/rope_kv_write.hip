@@ -66,6 +66,10 @@ template <> __device__ void store_vals<fp8e4m3>(void* p, const float* v, int n) 
   }
 }
 
+// One wave per token at a time (grid-stride over tokens): the token's slot,
+// cos/sin row and padding test are wave-uniform scalar loads, and the lanes
+// take the token's items — K vectors of rotate pairs, V vectors, Q vectors of
+// rotate pairs — 64 at a time.
 template <typename T, typename KV>
 __global__ void __launch_bounds__(256) rope_kv_write_kernel(RopeKVWriteArgs a) {
   constexpr int V = Elem<T>::kVec;
@@ -76,59 +80,63 @@ __global__ void __launch_bounds__(256) rope_kv_write_kernel(RopeKVWriteArgs a) {
   const int v_items = a.k ? a.num_kv_heads * dv : 0;
   const int q_items = a.q_out ? a.num_q_heads * pv : 0;
   const int per_tok = k_items + v_items + q_items;
-  const int64_t total = a.num_tokens * (int64_t)per_tok;
-  for (int64_t it = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; it < total;
-       it += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t tok = it / per_tok;
-    int u = (int)(it - tok * per_tok);
-    int64_t slot = -1;
-    bool write_kv = u < k_items + v_items;
-    if (write_kv) {
-      if (a.query_lens) {
-        int64_t b = tok / a.tokens_per_seq, r = tok - b * a.tokens_per_seq;
-        if (r >= a.query_lens[b]) continue;            // padded row: nothing to write
-      }
-      slot = a.slot_mapping[tok];
-      if (slot < 0 || slot >= a.num_slots) continue;   // never write out of the pool
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wpb = blockDim.x >> 6;
+  for (int64_t tok = (int64_t)blockIdx.x * wpb + wave; tok < a.num_tokens; tok += (int64_t)gridDim.x * wpb) {
+    // K/V of this token are written unless it is a padded row or its slot is
+    // outside the pool (never written); q is rotated either way
+    bool kv_ok = a.k != nullptr;
+    if (kv_ok && a.query_lens) {
+      const int64_t b = tok / a.tokens_per_seq, r = tok - b * a.tokens_per_seq;
+      kv_ok = r < a.query_lens[b];
     }
+    int64_t slot = -1;
+    if (kv_ok) {
+      slot = a.slot_mapping[tok];
+      kv_ok = slot >= 0 && slot < a.num_slots;
+    }
+    const int u0 = kv_ok ? 0 : k_items + v_items;
     const int64_t crow = a.rope_rows ? a.rope_rows[tok] : tok;
-    const char* cosp = reinterpret_cast<const char*>(a.cos) + crow * a.rope_row_stride * sizeof(T);
-    const char* sinp = reinterpret_cast<const char*>(a.sin) + crow * a.rope_row_stride * sizeof(T);
-    if (u < k_items || u >= k_items + v_items) {
-      // rotate one vector of pairs (x[j], x[j + D/2]) of K or Q
-      bool is_q = u >= k_items + v_items;
-      int uu = is_q ? u - k_items - v_items : u;
-      int h = uu / pv, j0 = (uu - h * pv) * V;
-      const char* src = reinterpret_cast<const char*>(is_q ? a.q : a.k) +
-                        (tok * (is_q ? a.q_row_stride : a.k_row_stride) + (int64_t)h * D) * sizeof(T);
-      float x1[V], x2[V], c[V], s[V], lo[V], hi[V];
-      Elem<T>::load(src + j0 * sizeof(T), x1);
-      Elem<T>::load(src + (j0 + half) * sizeof(T), x2);
-      Elem<T>::load(cosp + j0 * sizeof(T), c);
-      Elem<T>::load(sinp + j0 * sizeof(T), s);
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        // attention.py:105-118: [x1*c - x2*s, x1*s + x2*c], each op in T
-        lo[i] = Elem<T>::sub(Elem<T>::mul(x1[i], c[i]), Elem<T>::mul(x2[i], s[i]));
-        hi[i] = Elem<T>::add(Elem<T>::mul(x1[i], s[i]), Elem<T>::mul(x2[i], c[i]));
-      }
-      if (is_q) {
-        char* dst = reinterpret_cast<char*>(a.q_out) + (tok * a.q_out_row_stride + (int64_t)h * D) * sizeof(T);
-        store_vals<T>(dst + j0 * sizeof(T), lo, V);
-        store_vals<T>(dst + (j0 + half) * sizeof(T), hi, V);
+    for (int u = u0 + lane; u < per_tok; u += 64) {
+      const char* cosp = reinterpret_cast<const char*>(a.cos) + crow * a.rope_row_stride * sizeof(T);
+      const char* sinp = reinterpret_cast<const char*>(a.sin) + crow * a.rope_row_stride * sizeof(T);
+      if (u < k_items || u >= k_items + v_items) {
+        // rotate one vector of pairs (x[j], x[j + D/2]) of K or Q
+        bool is_q = u >= k_items + v_items;
+        int uu = is_q ? u - k_items - v_items : u;
+        int h = uu / pv, j0 = (uu - h * pv) * V;
+        const char* src = reinterpret_cast<const char*>(is_q ? a.q : a.k) +
+                          (tok * (is_q ? a.q_row_stride : a.k_row_stride) + (int64_t)h * D) * sizeof(T);
+        float x1[V], x2[V], c[V], s[V], lo[V], hi[V];
+        Elem<T>::load(src + j0 * sizeof(T), x1);
+        Elem<T>::load(src + (j0 + half) * sizeof(T), x2);
+        Elem<T>::load(cosp + j0 * sizeof(T), c);
+        Elem<T>::load(sinp + j0 * sizeof(T), s);
+  #pragma unroll
+        for (int i = 0; i < V; ++i) {
+          // attention.py:105-118: [x1*c - x2*s, x1*s + x2*c], each op in T
+          lo[i] = Elem<T>::sub(Elem<T>::mul(x1[i], c[i]), Elem<T>::mul(x2[i], s[i]));
+          hi[i] = Elem<T>::add(Elem<T>::mul(x1[i], s[i]), Elem<T>::mul(x2[i], c[i]));
+        }
+        if (is_q) {
+          char* dst = reinterpret_cast<char*>(a.q_out) + (tok * a.q_out_row_stride + (int64_t)h * D) * sizeof(T);
+          store_vals<T>(dst + j0 * sizeof(T), lo, V);
+          store_vals<T>(dst + (j0 + half) * sizeof(T), hi, V);
+        } else {
+          char* dst = reinterpret_cast<char*>(a.k_cache) + (slot * a.cache_slot_stride + (int64_t)h * D) * sizeof(KV);
+          store_vals<KV>(dst + j0 * sizeof(KV), lo, V);
+          store_vals<KV>(dst + (j0 + half) * sizeof(KV), hi, V);
+        }
       } else {
-        char* dst = reinterpret_cast<char*>(a.k_cache) + (slot * a.cache_slot_stride + (int64_t)h * D) * sizeof(KV);
-        store_vals<KV>(dst + j0 * sizeof(KV), lo, V);
-        store_vals<KV>(dst + (j0 + half) * sizeof(KV), hi, V);
+        int uu = u - k_items;
+        int h = uu / dv, j0 = (uu - h * dv) * V;
+        const char* src = reinterpret_cast<const char*>(a.v) + (tok * a.v_row_stride + (int64_t)h * D + j0) * sizeof(T);
+        float x[V];
+        Elem<T>::load(src, x);
+        char* dst = reinterpret_cast<char*>(a.v_cache) + (slot * a.cache_slot_stride + (int64_t)h * D + j0) * sizeof(KV);
+        store_vals<KV>(dst, x, V);
       }
-    } else {
-      int uu = u - k_items;
-      int h = uu / dv, j0 = (uu - h * dv) * V;
-      const char* src = reinterpret_cast<const char*>(a.v) + (tok * a.v_row_stride + (int64_t)h * D + j0) * sizeof(T);
-      float x[V];
-      Elem<T>::load(src, x);
-      char* dst = reinterpret_cast<char*>(a.v_cache) + (slot * a.cache_slot_stride + (int64_t)h * D + j0) * sizeof(KV);
-      store_vals<KV>(dst, x, V);
     }
   }
 }
@@ -137,9 +145,8 @@ hipError_t launch_rope_kv_write(const RopeKVWriteArgs& a, hipStream_t stream) {
   const int V = a.dtype == kF32 ? 4 : 8;
   const int64_t per_tok = (a.k ? (int64_t)a.num_kv_heads * (a.head_dim / 2 / V + a.head_dim / V) : 0) +
                           (a.q_out ? (int64_t)a.num_q_heads * (a.head_dim / 2 / V) : 0);
-  int64_t total = a.num_tokens * per_tok;
-  if (total == 0) return hipSuccess;
-  int64_t blocks = (total + 255) / 256;
+  if (a.num_tokens * per_tok == 0) return hipSuccess;
+  int64_t blocks = (a.num_tokens + 3) / 4;    // 4 waves of one token each
   if (blocks > 65536) blocks = 65536;
   dim3 grid((unsigned)blocks), block(256);
   if (a.dtype == kBF16 && a.kv_dtype == kBF16)
