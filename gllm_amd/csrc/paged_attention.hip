@@ -588,16 +588,15 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   const int64_t qrow = qstart + rr;
   const int qh = kvh * G + g;
 
-  // block ids of keys [0, kend_wg) -> LDS (first kBidCache blocks; any beyond
-  // are read from the table directly)
+  // Block ids of keys [0, kend_wg), loaded into registers now and cached in
+  // LDS (first kBidCache blocks; any beyond are read from the table
+  // directly) after the first tiles' copies are issued.
   const int32_t* bt = DENSE ? nullptr : a.block_table + (int64_t)seq * a.block_table_stride;
-  if (!DENSE) {
-    const int nblk = ((kend_wg - 1) >> a.block_shift) + 1;
-    for (int i = tid; i < min(nblk, Cfg::kBidCache); i += NT) {
-      const uint32_t b = (uint32_t)bt[i];
-      lbid[i] = b < (uint64_t)a.num_blocks ? (int32_t)b : 0;  // never address outside the pool
-    }
-  }
+  constexpr int KB = (Cfg::kBidCache + NT - 1) / NT;
+  const int nbc = DENSE ? 0 : min(((kend_wg - 1) >> a.block_shift) + 1, Cfg::kBidCache);
+  uint32_t lb[KB];
+#pragma unroll
+  for (int k = 0; k < KB; ++k) lb[k] = tid + k * NT < nbc ? (uint32_t)bt[tid + k * NT] : 0u;
 
   // Q rows (and their cos/sin rows): loads issued now, used after the first
   // K/V copies are on their way.
@@ -619,7 +618,6 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
     }
   }
   bf16x8 qB[NQ];                // filled once the first tile copies are issued
-  if (!DENSE) __syncthreads();  // block ids visible
 
   // Per-lane byte offsets inside a stage (tile-invariant; the stage and the
   // half / 16-key group go into the instructions' immediate offsets).
@@ -903,14 +901,36 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   static_assert(NS % 2 == 0 && TPB >= 1, "stage ring must hold two tile groups");
   const int ntiles = (kend_wg + BN - 1) / BN;
   const int full_end = ctx + r0;           // tiles ending at or before key ctx + r0 need no mask
-  uint32_t nbid[CHD];
+  // The first TPB tiles' copies are addressed with block ids read straight
+  // from the table (issued together with the loads above), so they need no
+  // trip through LDS and a barrier first; every load so far is waited for
+  // here explicitly, so nothing below waits on these copies by accident.
+  uint32_t fbid[TPB][CHD];
+#pragma unroll
+  for (int t = 0; t < TPB; ++t)
+#pragma unroll
+    for (int i = 0; i < CHD; ++i) {
+      fbid[t][i] = 0u;
+      if (!DENSE) {
+        const int p = min(t * BN + (i * NW + wave) * RPS + lane / CPR, kend_wg - 1);
+        fbid[t][i] = (uint32_t)bt[p >> a.block_shift];
+      }
+    }
+  wait_vmcnt<0>();
 #pragma unroll
   for (int t = 0; t < TPB; ++t)
     if (t < ntiles) {
-      dma_bids(t * BN, nbid);
-      dma_issue(t * BN, t, nbid);
+#pragma unroll
+      for (int i = 0; i < CHD; ++i)
+        if (fbid[t][i] >= (uint64_t)a.num_blocks) fbid[t][i] = 0u;  // never address outside the pool
+      dma_issue(t * BN, t, fbid[t]);
     }
-  if (TPB < ntiles) dma_bids(TPB * BN, nbid);
+  if (!DENSE) {
+#pragma unroll
+    for (int k = 0; k < KB; ++k)
+      if (tid + k * NT < nbc) lbid[tid + k * NT] = lb[k] < (uint64_t)a.num_blocks ? (int32_t)lb[k] : 0;
+  }
+  uint32_t nbid[CHD];
 
   // Q as the B operand of S^T = K Q^T: lane holds Q[row n][16kk + 8h + i].
   {
@@ -933,6 +953,8 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
       qB[kk] = to_bf16x8(x[kk]);
     }
   }
+  if (!DENSE) __syncthreads();  // block ids in LDS visible
+  if (TPB < ntiles) dma_bids(TPB * BN, nbid);
 
   for (int t0 = 0; t0 < ntiles; t0 += TPB) {
     wait_vmcnt<0>();                       // this thread's copies of tiles t0 .. t0+TPB-1
