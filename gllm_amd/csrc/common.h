@@ -49,6 +49,22 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(pack_bf16x2(f, 0.f) & 0xffffu); }
+// Two values rounded the same way with one convert.
+__device__ __forceinline__ void round2_bf16(float& a, float& b) {
+  const uint32_t w = pack_bf16x2(a, b);
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xffff0000u);
+}
+// One rotate-half pair, each op rounded to bf16 like the reference's torch ops
+// (gllm/model/layers/attention.py:105-118): [x1 c - x2 s, x1 s + x2 c].
+__device__ __forceinline__ void rope_pair_bf16(float& x1, float& x2, float c, float s) {
+  float a = __fmul_rn(x1, c), b = __fmul_rn(x2, s), e = __fmul_rn(x1, s), f = __fmul_rn(x2, c);
+  round2_bf16(a, b);
+  round2_bf16(e, f);
+  x1 = __fsub_rn(a, b);
+  x2 = __fadd_rn(e, f);
+  round2_bf16(x1, x2);
+}
 
 // 8 fp32 -> one MFMA operand of 8 bf16.
 __device__ __forceinline__ bf16x8 to_bf16x8(const float* v) {

@@ -29,14 +29,7 @@ namespace gllm {
 // torch ops (gllm/model/layers/attention.py:105-118).
 __device__ __forceinline__ void rope8_bf16(float* x1, float* x2, const float* c, const float* s) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float a = round_bf16(__fmul_rn(x1[i], c[i]));
-    float b = round_bf16(__fmul_rn(x2[i], s[i]));
-    float e = round_bf16(__fmul_rn(x1[i], s[i]));
-    float f = round_bf16(__fmul_rn(x2[i], c[i]));
-    x1[i] = round_bf16(__fsub_rn(a, b));
-    x2[i] = round_bf16(__fadd_rn(e, f));
-  }
+  for (int i = 0; i < 8; ++i) rope_pair_bf16(x1[i], x2[i], c[i], s[i]);
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 w) { return __builtin_bit_cast(bf16x8, w); }
@@ -203,10 +196,16 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
           unpack_bf16x8(sraw[kk], s);
           unpack_bf16x8(praw[kk], xp);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float u = round_bf16(__fmul_rn(x[kk][i], c[i]));
-            const float v = round_bf16(__fmul_rn(xp[i], s[i]));
-            x[kk][i] = round_bf16(first ? __fsub_rn(u, v) : __fadd_rn(u, v));
+          for (int i = 0; i < 8; i += 2) {
+            float u0 = __fmul_rn(x[kk][i], c[i]), v0 = __fmul_rn(xp[i], s[i]);
+            float u1 = __fmul_rn(x[kk][i + 1], c[i + 1]), v1 = __fmul_rn(xp[i + 1], s[i + 1]);
+            round2_bf16(u0, v0);
+            round2_bf16(u1, v1);
+            float r0 = first ? __fsub_rn(u0, v0) : __fadd_rn(u0, v0);
+            float r1 = first ? __fsub_rn(u1, v1) : __fadd_rn(u1, v1);
+            round2_bf16(r0, r1);
+            x[kk][i] = r0;
+            x[kk][i + 1] = r1;
           }
         }
       }

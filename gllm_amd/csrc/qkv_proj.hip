@@ -32,16 +32,6 @@ namespace gllm {
 
 namespace {
 
-// One rotate-half pair, each op rounded to bf16 (attention.py:105-118).
-__device__ __forceinline__ void rope1_bf16(float& x1, float& x2, float c, float s) {
-  const float a = round_bf16(__fmul_rn(x1, c));
-  const float b = round_bf16(__fmul_rn(x2, s));
-  const float e = round_bf16(__fmul_rn(x1, s));
-  const float f = round_bf16(__fmul_rn(x2, c));
-  x1 = round_bf16(__fsub_rn(a, b));
-  x2 = round_bf16(__fadd_rn(e, f));
-}
-
 // XCD-grouped order of the large-batch tiles: workgroup b of the launch runs
 // on XCD b % kXcds, and each XCD takes super-groups of gt token tiles x gh
 // head groups (gt * gh = the workgroups one XCD holds at once), so the
@@ -261,11 +251,15 @@ qkv_rope_write_kernel(QKVArgs a) {
   for (int j = 0; j < 16; ++j) {
     float v[NB];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) v[b] = round_bf16(acc[r][b][j]);  // F.linear's bf16 output
+    for (int b = 0; b < NB; b += 2) {                              // F.linear's bf16 output
+      v[b] = acc[r][b][j];
+      v[b + 1] = acc[r][b + 1][j];
+      round2_bf16(v[b], v[b + 1]);
+    }
     if (rope) {
 #pragma unroll
       for (int b = 0; b < NH; ++b)
-        rope1_bf16(v[b], v[b + NH], bf16_bits_to_f32(csn[j][b] & 0xffffu), bf16_bits_to_f32(csn[j][b] >> 16));
+        rope_pair_bf16(v[b], v[b + NH], bf16_bits_to_f32(csn[j][b] & 0xffffu), bf16_bits_to_f32(csn[j][b] >> 16));
     }
     if (dst[j] < 0) continue;
     if (KV8 && to_cache) {
@@ -410,13 +404,12 @@ __global__ void __launch_bounds__(256) qkv_finish_kernel(QKVArgs a) {
     x1 += ws[(int64_t)c * a.num_tokens * F];
     x2 += ws[(int64_t)c * a.num_tokens * F + PPH];
   }
-  x1 = round_bf16(x1);
-  x2 = round_bf16(x2);
+  round2_bf16(x1, x2);
   if (kind == 1 || (kind == 0 && a.rotate_q)) {
     const int64_t crow = a.rope_rows ? a.rope_rows[tok] : tok;
     const float c = bf16_bits_to_f32(((const uint16_t*)a.cos)[crow * a.rope_row_stride + d]);
     const float sn = bf16_bits_to_f32(((const uint16_t*)a.sin)[crow * a.rope_row_stride + d]);
-    rope1_bf16(x1, x2, c, sn);
+    rope_pair_bf16(x1, x2, c, sn);
   }
   if (kind == 0) {
     uint16_t* op = (uint16_t*)a.q_out + tok * a.q_out_row_stride + (int64_t)h * D + d;

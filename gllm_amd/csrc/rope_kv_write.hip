@@ -19,17 +19,19 @@ template <> struct Elem<float> {
     u32x4 w = ld16(p);
     for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(w[i]);
   }
-  __device__ static float mul(float a, float b) { return __fmul_rn(a, b); }
-  __device__ static float add(float a, float b) { return __fadd_rn(a, b); }
-  __device__ static float sub(float a, float b) { return __fsub_rn(a, b); }
+  // attention.py:105-118: [x1*c - x2*s, x1*s + x2*c], no contraction
+  __device__ static void rope(float& x1, float& x2, float c, float s) {
+    const float lo = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
+    const float hi = __fadd_rn(__fmul_rn(x1, s), __fmul_rn(x2, c));
+    x1 = lo;
+    x2 = hi;
+  }
 };
 template <> struct Elem<__bf16> {
   static constexpr int kVec = 8;
   __device__ static void load(const void* p, float* v) { unpack_bf16x8(ld16(p), v); }
-  // bf16 x bf16 is exact in fp32; the store rounds once (RNE), like torch.
-  __device__ static float mul(float a, float b) { return round_bf16(__fmul_rn(a, b)); }
-  __device__ static float add(float a, float b) { return round_bf16(__fadd_rn(a, b)); }
-  __device__ static float sub(float a, float b) { return round_bf16(__fsub_rn(a, b)); }
+  // the same with every op rounded to bf16 (RNE), like torch's bf16 ops
+  __device__ static void rope(float& x1, float& x2, float c, float s) { rope_pair_bf16(x1, x2, c, s); }
 };
 
 // Store `n` values (already representable in T when T is the model dtype)
@@ -115,9 +117,9 @@ __global__ void __launch_bounds__(256) rope_kv_write_kernel(RopeKVWriteArgs a) {
         Elem<T>::load(sinp + j0 * sizeof(T), s);
   #pragma unroll
         for (int i = 0; i < V; ++i) {
-          // attention.py:105-118: [x1*c - x2*s, x1*s + x2*c], each op in T
-          lo[i] = Elem<T>::sub(Elem<T>::mul(x1[i], c[i]), Elem<T>::mul(x2[i], s[i]));
-          hi[i] = Elem<T>::add(Elem<T>::mul(x1[i], s[i]), Elem<T>::mul(x2[i], c[i]));
+          lo[i] = x1[i];
+          hi[i] = x2[i];
+          Elem<T>::rope(lo[i], hi[i], c[i], s[i]);   // each op in T
         }
         if (is_q) {
           char* dst = reinterpret_cast<char*>(a.q_out) + (tok * a.q_out_row_stride + (int64_t)h * D) * sizeof(T);
