@@ -17,10 +17,10 @@
 // K-slices of 32 stream HBM/L2 -> LDS with global_load_lds into a 4-stage
 // ring (XOR-swizzled 16-byte chunks: operand reads are bank-conflict free);
 // each wave computes 32 tokens x D outputs per row block on
-// v_mfma_f32_32x32x16_bf16 (D/32 accumulator blocks).  Output column n of block b is head dim
-// 32b + n, so a RoPE pair (d, d + D/2) sits in blocks b and b + D/64 of the
-// same lane: the rotation happens in registers and every value is stored
-// from its lane (2-byte stores, 64-byte runs per half-wave).  Batches too
+// v_mfma_f32_32x32x16_bf16 (D/32 accumulator blocks).  Output column n of
+// block b is head dim 32b + n, so a RoPE pair (d, d + D/2) sits in blocks b
+// and b + D/64 of the same lane: the rotation happens in registers and every
+// value is stored from its lane (2-byte stores, 64-byte runs per half-wave).  Batches too
 // small to fill the GPU with such tiles split the hidden dimension
 // (qkv_partial_kernel + qkv_finish_kernel, below).
 #include <algorithm>
