@@ -259,6 +259,37 @@ def test_dense_op_engine_bias_and_masked_rows(dtype):
     assert d.max().item() < tol
 
 
+@pytest.mark.parametrize("k", range(12))
+def test_dense_op_random_bias(k):
+    """reference_attention with arbitrary additive biases (finite values of
+    either sign plus scattered -inf, every row keeping a finite entry), seeded
+    random shapes, bf16 and fp32."""
+    import random
+    r = random.Random(500 + k)
+    B, Tq = r.randint(1, 4), r.randint(1, 100)
+    T = Tq + r.randint(0, 200)
+    Hkv = r.choice([1, 2, 4])
+    Hq = Hkv * r.choice([1, 2, 4, 8])
+    D = r.choice([64, 128])
+    dtype = r.choice([torch.float32, torch.bfloat16])
+    print(f"dense random {k}: B={B} Tq={Tq} T={T} Hq={Hq} Hkv={Hkv} D={D} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(600 + k)
+    q = torch.randn(B, Tq, Hq, D, generator=g).to(dtype)
+    kk = torch.randn(B, T, Hkv, D, generator=g).to(dtype)
+    v = torch.randn(B, T, Hkv, D, generator=g).to(dtype)
+    bias = 3.0 * torch.randn(B, Tq, T, generator=g)
+    bias[torch.rand(B, Tq, T, generator=g) < 0.3] = float("-inf")
+    bias[..., 0] = torch.randn(B, Tq, generator=g)          # a finite entry in every row
+    bias = bias.to(dtype)
+    ref = oa.reference_attention(q.float(), kk.float(), v.float(), bias.float())
+    out = gllm_amd.reference_attention(q.to(DEV), kk.to(DEV), v.to(DEV), bias.to(DEV))
+    torch.cuda.synchronize()
+    if dtype == torch.float32:
+        assert (out.cpu() - ref).abs().max().item() < 1e-4
+    else:
+        assert_close_bf16(out, ref, "dense random bias")
+
+
 # ------------------------------------------------------------ call-site drop-in
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_attention_forward_dropin(dtype):
