@@ -135,7 +135,9 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
 // lds_base + 16 l (lds_base wave-uniform, in M0).  Written as inline asm so
 // the compiler does not wait for every outstanding copy before each LDS read;
 // the kernel waits for its own copies with wait_vmcnt before the barrier that
-// publishes a stage.
+// publishes a stage.  M0 is set inside the asm and listed as clobbered (the
+// compiler warns that it reserves M0; in these kernels every M0 write in the
+// generated code is this asm's own, checked in the assembly).
 __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_base) : "memory", "m0");
 }
