@@ -770,7 +770,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
       for (int j = 0; j < 16; ++j) s[j] -= q.dlt;
     }
   };
-  auto sm_exp = [&](f32x16& s, int j0, const Soft& q) {
+  auto sm_exp = [&](f32x16& s, int j0) {
 #pragma unroll
     for (int j = j0; j < j0 + 4; ++j) s[j] = fast_exp2(s[j]);
   };
@@ -793,7 +793,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   // Logical softmax piece p (0..7) of a half: max, 4 x exp, sum, convert.
   auto sm_piece = [&](int p, f32x16& s, int k0, bool mask, Soft& q, bf16x8* pb) {
     if (p == 0) sm_max(s, k0, mask, q);
-    else if (p <= 4) sm_exp(s, 4 * (p - 1), q);
+    else if (p <= 4) sm_exp(s, 4 * (p - 1));
     else if (p == 5) sm_sum(s, q);
     else if (p == 6) sm_cvt(s, pb);
   };
