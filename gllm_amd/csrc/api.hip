@@ -118,9 +118,12 @@ BalancedShape balanced_shape(const gllm_attn_plan* p, int cus, int heads_req) {
 // Page-balanced plans pay a partial write, an L2 write-back (agent-scope
 // release) and a ticket per segment, and the merges of the last segments
 // sit on the launch's tail: measured on MI355X this wins when a workgroup
-// streams at least ~2048 keys (long-context batches) and loses to the
-// split planner below that.
-constexpr int64_t kBalancedMinUnitsPerWg = 128;
+// streams enough keys and loses to the split planner below that.  D=64:
+// from ~2048 keys (128 units) per workgroup.  D=128 (Hkv 8, one workgroup per
+// CU): the split planner is 3-3.5% faster at 128-137 units per workgroup, the
+// two are within 1% from 248 to 514, and page-balanced is 0.6-5% faster at
+// 740-770; the cut sits between the measured points.
+int64_t balanced_min_units_per_wg(int D) { return D == 128 ? 192 : 128; }
 
 void plan_balanced_decode(gllm_attn_plan* p, int cus, int heads_req) {
   const BalancedShape shape = balanced_shape(p, cus, heads_req);
@@ -375,7 +378,7 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
     bool balanced = split_tokens == GLLM_SPLIT_BALANCED && num_seqs > 0;
     if (n_pf == 0 && split_tokens == 0 && num_seqs > 0) {
       const BalancedShape bsh = balanced_shape(p, cus, decode_heads_per_wg);
-      balanced = bsh.units >= kBalancedMinUnitsPerWg * bsh.wgs;
+      balanced = bsh.units >= balanced_min_units_per_wg(p->D) * bsh.wgs;
     }
     if (balanced) {
       plan_balanced_decode(p, cus, decode_heads_per_wg);

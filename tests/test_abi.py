@@ -93,6 +93,15 @@ def test_planner_page_balanced():
     assert rc == 0 and i["wgs"] == 256 and i["segs"] >= 256 and i["hw"] == 8
     # a segment caches at most 512 block ids: >= 8192 keys per workgroup means cuts
     assert i["segs"] >= sum(-(-L // 8192) for L in e.seq_lens)
+    # D = 128: the balanced plan needs >= 192 units (3072 keys) per workgroup,
+    # so (d)'s 256 decodes (~137 units per workgroup) stay on the split planner
+    d = workloads.config_d()
+    rc, i = _plan_info(lib, d.q_lens[:256], d.seq_lens[:256], 32, 8, 128)
+    assert rc == 0 and i["segs"] == 0 and i["split"] > 0
+    rc, i = _plan_info(lib, [1] * 256, [191 * 16] * 256, 32, 8, 128)
+    assert rc == 0 and i["segs"] == 0
+    rc, i = _plan_info(lib, [1] * 256, [192 * 16] * 256, 32, 8, 128)
+    assert rc == 0 and i["segs"] == 256 and i["wgs"] == 256
     # prefill-path sequences cannot be planned page-balanced
     rc, _ = _plan_info(lib, [1, 40], [100, 80], 32, 8, 64, split=-1)
     assert rc == _lib.EINVAL and b"decode-only" in lib.gllm_attn_last_error()
