@@ -814,8 +814,9 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   };
 
   // st: the tile's stage (K at +0, V at +kTile).  The tile is scheduled by
-  // hand (sched_barrier fences keep the source order): (1) K reads, S^T of
-  // half 0, then the MFMAs of S^T half 1 each followed by two V reads of half
+  // hand (sched_barrier fences keep the source order): (1) K reads of half 0,
+  // S^T of half 0 with the K reads of half 1 between its MFMAs, then the
+  // MFMAs of S^T half 1 each followed by two V reads of half
   // 0 and one softmax piece of half 0; (2) the MFMAs of O^T += V^T P^T half 0,
   // each followed by V reads and a softmax piece of half 1; (3) P V of half 1.
   // One wave thus keeps the matrix core busy while its own VALU work runs;
@@ -827,14 +828,18 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
     Soft q0, q1;
     u32x4 ka[2][NQ];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int kk = 0; kk < NQ; ++kk) ka[kb][kk] = *reinterpret_cast<const u32x4*>(st + kb * 32 * RW + koff[kk]);
+    for (int kk = 0; kk < NQ; ++kk) ka[0][kk] = *reinterpret_cast<const u32x4*>(st + koff[kk]);
     sbase = m == kNegInf ? 0.f : -m;     // both halves start from the max before this tile
 #pragma unroll
     for (int j = 0; j < 16; ++j) s0[j] = sbase, s1[j] = sbase;
+    // K of half 1 is read between the MFMAs of half 0: the eight waves' reads
+    // after a barrier do not all hit LDS at once, and fewer registers are live
 #pragma unroll
-    for (int kk = 0; kk < NQ; ++kk) s0 = mfma32(as_bf16x8(ka[0][kk]), qB[kk], s0);
+    for (int kk = 0; kk < NQ; ++kk) {
+      s0 = mfma32(as_bf16x8(ka[0][kk]), qB[kk], s0);
+      ka[1][kk] = *reinterpret_cast<const u32x4*>(st + 32 * RW + koff[kk]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     // region 1: S^T half 1 | V reads half 0 | softmax half 0
     constexpr int V_PER = 2 * NO / NQ;           // V operand reads (pairs) per slot
 #pragma unroll
