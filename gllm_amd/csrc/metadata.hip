@@ -2,12 +2,17 @@
 // gllm/llm/llm.py:245-281 builds on the host with a per-row Python loop (and
 // a dense O(B*T_q*T) bias that the paged kernels do not need).
 //
-// For query row r of sequence i (c_i = seq_len_i - query_len_i):
-//   position = c_i + r                                   (llm.py:281, padded rows too)
+// For query row r of sequence i (c_i = seq_len_i - query_len_i, L_i = seq_len_i):
+//   position = c_i + r                                   if r < q_i (llm.py:281)
+//              L_i - 1 (the last real position)           otherwise (padded rows)
 //   slot     = block_table[i][(c_i + r) / bs] * bs + (c_i + r) % bs   if r < q_i
 //              0 (the reserved dummy slot)                             otherwise
 // which is what llm.py:245-247, 259-268 and 277 produce for the query
-// columns of the left-padded slot mapping.  Packed layout: sequence i's rows
+// columns of the left-padded slot mapping.  llm.py:281 gives padded rows
+// c_i + r as well; in a mixed batch that can pass the RoPE table's last row
+// (model.py:195 then indexes out of range), so padded rows are clamped to the
+// sequence's last position: every position stays below max(seq_len), and
+// real rows are unchanged.  Packed layout: sequence i's rows
 // start at cu_seqlens[i] = q_0 + ... + q_{i-1}.
 #include "common.h"
 #include "launch.h"
@@ -50,7 +55,8 @@ __global__ void __launch_bounds__(256) build_metadata_kernel(MetadataArgs a) {
   for (int64_t r = tid; r < nrows; r += 256) {
     const int64_t row = start + r;
     if (row >= a.num_rows) break;
-    const int64_t pos = c + r;
+    // padded rows: the last real position (0 for an empty sequence)
+    const int64_t pos = r < q ? c + r : (L > 0 ? (int64_t)L - 1 : 0);
     int64_t slot = 0;
     if (ok && r < q) {
       const int64_t bi = pos >> a.block_shift;

@@ -214,10 +214,15 @@ qkv_rope_write_kernel(QKVArgs a) {
     if (kind != 0) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) slot[j] = a.slot_mapping[tc[j]];
-      if (a.query_lens) {
+    }
+    if (a.query_lens) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) qlen[j] = a.query_lens[tc[j] / a.tokens_per_seq];
-      }
+      for (int j = 0; j < 16; ++j) qlen[j] = a.query_lens[tc[j] / a.tokens_per_seq];
+      // padded rows read cos/sin row 0 (their own position may lie past the
+      // table in mixed batches) and are not written below
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (tc[j] % a.tokens_per_seq >= qlen[j]) crow[j] = 0;
     }
     if (rope) {
 #pragma unroll
@@ -232,14 +237,14 @@ qkv_rope_write_kernel(QKVArgs a) {
     for (int j = 0; j < 16; ++j) {
       const int64_t tok = tbase + 8 * (j / 4) + (j % 4);
       int64_t d = -1;
-      if (tok < N) {
+      // padded rows of the reference's [B, T_q] layout are not written (q
+      // included); slots outside the pool are never addressed
+      const bool real = !a.query_lens || tok % a.tokens_per_seq < qlen[j];
+      if (tok < N && real) {
         if (kind == 0) {
           if (a.q_out) d = tok * a.q_out_row_stride + (int64_t)h * D;
         } else {
-          // padded rows of the reference's [B, T_q] layout are not cached;
-          // slots outside the pool are never addressed
-          const bool real = !a.query_lens || tok % a.tokens_per_seq < qlen[j];
-          if (real && slot[j] >= 0 && slot[j] < a.num_slots) d = slot[j] * a.cache_slot_stride + (int64_t)h * D;
+          if (slot[j] >= 0 && slot[j] < a.num_slots) d = slot[j] * a.cache_slot_stride + (int64_t)h * D;
         }
       }
       dst[j] = d;
@@ -405,6 +410,8 @@ __global__ void __launch_bounds__(256) qkv_finish_kernel(QKVArgs a) {
     x2 += ws[(int64_t)c * a.num_tokens * F + PPH];
   }
   round2_bf16(x1, x2);
+  // padded rows of the [B, T_q] layout: nothing written, cos/sin not read
+  if (a.query_lens && tok % a.tokens_per_seq >= a.query_lens[tok / a.tokens_per_seq]) return;
   if (kind == 1 || (kind == 0 && a.rotate_q)) {
     const int64_t crow = a.rope_rows ? a.rope_rows[tok] : tok;
     const float c = bf16_bits_to_f32(((const uint16_t*)a.cos)[crow * a.rope_row_stride + d]);
@@ -417,7 +424,6 @@ __global__ void __launch_bounds__(256) qkv_finish_kernel(QKVArgs a) {
     op[PPH] = (uint16_t)pack_bf16x2(x2, 0.f);
     return;
   }
-  if (a.query_lens && tok % a.tokens_per_seq >= a.query_lens[tok / a.tokens_per_seq]) return;
   const int64_t slot = a.slot_mapping[tok];
   if (slot < 0 || slot >= a.num_slots) return;
   char* cp = (char*)(kind == 1 ? a.k_cache : a.v_cache) + (slot * a.cache_slot_stride + (int64_t)h * D + d) * (KV8 ? 1 : 2);

@@ -86,13 +86,17 @@ __global__ void __launch_bounds__(256) rope_kv_write_kernel(RopeKVWriteArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wpb = blockDim.x >> 6;
   for (int64_t tok = (int64_t)blockIdx.x * wpb + wave; tok < a.num_tokens; tok += (int64_t)gridDim.x * wpb) {
-    // K/V of this token are written unless it is a padded row or its slot is
-    // outside the pool (never written); q is rotated either way
-    bool kv_ok = a.k != nullptr;
-    if (kv_ok && a.query_lens) {
+    // Padded rows of the reference's [B, T_q] layout (r >= query_lens[b])
+    // are skipped whole: no K/V write (the reference sends them to dummy slot
+    // 0) and no q rotation, so their cos/sin rows are never read (their
+    // positions may lie past the table in mixed batches); their q_out rows
+    // are left as they are.  K/V of a real row are written unless its slot is
+    // outside the pool (never written).
+    if (a.query_lens) {
       const int64_t b = tok / a.tokens_per_seq, r = tok - b * a.tokens_per_seq;
-      kv_ok = r < a.query_lens[b];
+      if (r >= a.query_lens[b]) continue;
     }
+    bool kv_ok = a.k != nullptr;
     int64_t slot = -1;
     if (kv_ok) {
       slot = a.slot_mapping[tok];

@@ -70,7 +70,10 @@ int gllm_attn_version(void);
 /*
  * Query-row metadata on the device (gllm/llm/llm.py:245-281).  For query row
  * r of sequence i, with c_i = seq_lens[i] - query_lens[i]:
- *   positions[row]    = c_i + r                       (padded rows too, as llm.py:281)
+ *   positions[row]    = c_i + r for r < query_lens[i] (llm.py:281); padded rows get the
+ *                       sequence's last position seq_lens[i] - 1 (llm.py:281 gives them
+ *                       c_i + r, which can pass the RoPE table's end in mixed batches),
+ *                       so every position is < max(seq_lens) and indexes the table.
  *   slot_mapping[row] = block_table[i][(c_i+r)/bs]*bs + (c_i+r)%bs for r < query_lens[i],
  *                       0 (the reserved dummy slot) for padded rows, as llm.py:277 gives.
  * q_seq_stride > 0: padded layout, row = i*q_seq_stride + r for r < q_seq_stride.
@@ -95,7 +98,7 @@ int gllm_build_metadata(const int32_t* block_table, int64_t block_table_stride, 
  * (bf16 or fp8 e4m3fn).  q is written to q_out if q_out != NULL (rotated or
  * not: the paged attention kernels can rotate it on load).  query_lens /
  * tokens_per_seq / rope_rows and the slot range check as in
- * gllm_rope_kv_write.  hidden must be a positive multiple of 32; x, the
+ * gllm_rope_kv_write (padded rows: nothing written, q_out included).  hidden must be a positive multiple of 32; x, the
  * weights and their row strides 16-byte aligned.  workspace (may be NULL,
  * 16-byte aligned) see gllm_qkv_workspace_bytes.  Results equal the
  * reference within the GEMM's accumulation order (fp32 sums in another
@@ -128,7 +131,9 @@ size_t gllm_qkv_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t num_
  * slot_mapping[t] of k_cache / v_cache (each [num_slots, cache_slot_stride]).
  * If query_lens != NULL, token t is row t % tokens_per_seq of sequence
  * t / tokens_per_seq and rows past query_lens[seq] (the reference's padded
- * rows, which it sends to dummy slot 0) are skipped.  Slots outside
+ * rows, which it sends to dummy slot 0) are skipped whole: nothing is
+ * written for them (their q_out rows included) and their cos/sin rows are
+ * not read.  Slots outside
  * [0, num_slots) are never written.  cos/sin rows: rope_rows[t] if given,
  * else t.  dtype is the model dtype of q/k/v/cos/sin; kv_dtype the cache's
  * (the model dtype, bf16 under f32, or fp8 e4m3fn: rounded like torch's

@@ -67,7 +67,7 @@ class Metadata:
     slot_mapping: torch.Tensor        # [B, T] int64 (left-padded)
     query_slot_mapping: torch.Tensor  # [B, T_q] int64
     bias: torch.Tensor                # [B, T_q, T] model dtype, 0 / -inf
-    positions: torch.Tensor           # [B, T_q] int64
+    positions: torch.Tensor           # [B, T_q] int64 (padded rows: L_i - 1)
 
 
 def build_metadata(
@@ -110,9 +110,15 @@ def build_metadata(
     qb = bias[:, :, max_ctx:]
     qb.fill_(float("-inf"))
     qb.triu_(diagonal=1)
-    # llm.py:277, 281.
+    # llm.py:277, 281.  llm.py:281 gives padded rows (r >= q_i) the position
+    # c_i + r too; in a mixed batch that can pass the RoPE table's last row
+    # (model.py:195 then raises IndexError).  Padded rows are clamped to the
+    # sequence's last position L_i - 1 here, as the product does; real rows
+    # keep c_i + r exactly.
     qsm = padded[:, -max_q:].contiguous()
     positions = ctx.to(torch.int64).unsqueeze(1) + torch.arange(max_q, dtype=torch.int64)
+    real = torch.arange(max_q).unsqueeze(0) < q.unsqueeze(1)
+    positions = torch.where(real, positions, (seq.to(torch.int64) - 1).clamp(min=0).unsqueeze(1))
     return Metadata(
         query_lens=q, seq_lens=seq.to(torch.int32), max_seq_len=seq.max().to(torch.int32),
         block_table=bt, slot_mapping=padded, query_slot_mapping=qsm, bias=bias,

@@ -63,6 +63,22 @@ def test_metadata_packed_matches_oracle(k):
     assert cu.cpu().tolist() == [0] + np.cumsum(ql).tolist()
 
 
+def test_metadata_padded_positions_clamped():
+    # decode rows padded to a 512-row chunk: c_i + T_q - 1 passes max(seq_len),
+    # the kernel clamps padded rows to seq_len - 1 like the oracle
+    ctx, ql, bs = [8000, 100, 3000, 0], [1, 512, 1, 3], 16
+    bt, meta = _case(ctx, ql, bs, seed=9)
+    B, Tq = len(ql), max(ql)
+    sl = torch.tensor([c + q for c, q in zip(ctx, ql)], dtype=torch.int32, device=DEV)
+    qd = torch.tensor(ql, dtype=torch.int32, device=DEV)
+    slots, pos, _ = paged.build_metadata(torch.from_numpy(bt).to(DEV), sl, qd, bs, q_seq_stride=Tq)
+    torch.cuda.synchronize()
+    p = pos.cpu().view(B, Tq)
+    assert torch.equal(p, meta.positions)
+    assert int(p.max()) == max(c + q for c, q in zip(ctx, ql)) - 1
+    assert p[0].tolist() == [8000] * Tq and p[3].tolist() == [0, 1, 2] + [2] * (Tq - 3)
+
+
 def test_metadata_never_reads_past_table():
     # a sequence whose length needs more blocks than the table holds: the
     # missing columns give slot 0 instead of reading beyond the row

@@ -54,7 +54,7 @@ def test_rope_kv_write_bit_exact(dtype, kv_dtype, D):
     oa.kv_write(kc_ref, vc_ref, meta.query_slot_mapping, k_ref, v)
     # product
     kc, vc = sentinel_k.to(DEV), sentinel_v.to(DEV)
-    q_out = torch.empty(B, Tq, Hq, D, dtype=dtype, device=DEV)
+    q_out = torch.full((B, Tq, Hq, D), 7.0, dtype=dtype, device=DEV)
     paged.rope_kv_write(k.to(DEV), v.to(DEV), cos.to(DEV), sin.to(DEV), kc, vc,
                         meta.query_slot_mapping.to(DEV), query_lens=meta.query_lens.to(DEV),
                         q=q.to(DEV), q_out=q_out)
@@ -65,6 +65,7 @@ def test_rope_kv_write_bit_exact(dtype, kv_dtype, D):
     assert torch.equal(_bits(kc)[:bs], _bits(sentinel_k)[:bs])  # padded rows skipped
     for i in range(B):
         assert torch.equal(_bits(q_out[i, :ql[i]]), _bits(q_ref[i, :ql[i]]))
+        assert bool((q_out[i, ql[i]:] == 7.0).all())   # padded rows: not written, cos/sin not read
     # apply_rope drop-in on a whole tensor
     qr = paged.rope_rotate(q.to(DEV), cos.to(DEV), sin.to(DEV))
     assert torch.equal(_bits(qr), _bits(q_ref))

@@ -57,9 +57,28 @@ def test_metadata_bruteforce(seed):
                 if r < q[i] and not (0 <= p < L):
                     assert want == -math.inf
         for r in range(max_q):
-            assert int(m.positions[i, r]) == ctx[i] + r
+            # llm.py:281 on real rows; padded rows clamped to the last real position
+            assert int(m.positions[i, r]) == (ctx[i] + r if r < q[i] else L - 1)
             want = om.slot_of(bt[i], ctx[i] + r, bs) if r < q[i] else 0
             assert int(m.query_slot_mapping[i, r]) == want
+
+
+def test_padded_positions_stay_inside_the_rope_table():
+    # a mixed batch: decode rows padded to the prefill chunk's T_q.  llm.py:281
+    # would give the decode rows positions up to c_i + T_q - 1 (past the end of
+    # a max_seq_len-row RoPE table); the clamp keeps every position < max L_i
+    ctx, ql, bs = [8000, 100, 3000], [1, 512, 1], 16
+    max_seq_len = max(c + q for c, q in zip(ctx, ql))           # 8001 rows of cos/sin
+    g = torch.Generator().manual_seed(5)
+    bt = om.random_block_tables([c + q for c, q in zip(ctx, ql)], bs, 1200, g)
+    m = om.build_metadata(ctx, ql, bt, bs)
+    assert ctx[0] + max(ql) - 1 >= max_seq_len                   # the unclamped value would overflow
+    assert int(m.positions.max()) == max_seq_len - 1
+    assert m.positions[0].tolist() == [8000] * 512               # decode row 0 real, rows 1.. padded
+    assert m.positions[1].tolist() == list(range(100, 612))      # the chunk: all real
+    assert m.positions[2].tolist() == [3000] * 512
+    cos = torch.randn(max_seq_len, 32)
+    assert cos[m.positions].shape == (3, 512, 32)                # model.py:195's gather is in range
 
 
 def test_metadata_invariants():
