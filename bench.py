@@ -1,21 +1,28 @@
 """Benchmark of the gLLM attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs b,c,d,e]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs d,c,b,e]
 
-Prints ONE JSON line.  The headline (``value``) is BASELINE config (b): decode
-paged attention at the Llama-3.2-1B head shape, in GB/s of compulsory HBM
-bytes per launch, inputs resident in HBM, KV pools rotated so the 256 MB
-Infinity Cache cannot serve them (cold HBM).  A "step" is one attention launch
-over the whole batch (one layer's attention).  Configs (c)-(e) are reported
-in ``extra`` with their own roofline figures; (c)'s step also includes the
-fused RoPE + KV write kernel.  The CPU baseline times the reference's path
-(padded gather, GQA expand, dense softmax attention, fp32 torch) on the
-host's cores for config (b).
+Prints ONE JSON line.  The headline (``value``) is BASELINE config (d), the
+metric's 8B GQA shape: one paged-attention launch over a mixed continuous
+batch (256 decode sequences + 4 chunked prefills of 512 tokens, Llama-3.1-8B
+heads), in GB/s of compulsory HBM bytes per launch, inputs resident in HBM.
+A "step" is that launch (one layer's attention over the batch).  Timing: a
+few steps are captured in one HIP graph (so graph-launch gaps do not count
+as kernel time) and the graph is replayed K times (K >= 50 by default), each
+replay bracketed by HIP events on the stream the kernels run on; the
+reported step time is the median over the replays of replay time / steps.  Configs (c) prefill
+(TFLOP/s against the bf16 MFMA peak), (d)'s decodes alone, (e) long decode
+and (b) 1B decode are reported in ``extra``, each with its own roofline and
+CPU-baseline objects.  The CPU baseline times the reference's path (dense KV
+gather through the slot mapping, GQA expand, softmax attention with the
+0/-inf bias; fp32 torch on every host core) per sequence (B = 1, no padding)
+and sums, on the same inputs copied from the GPU.
 """
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import platform
 import statistics
@@ -33,127 +40,148 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 
 
-def _events_time(launches, warmup, steps):
-    """Run ``launches[i % len]`` warmup + steps times on the current stream;
-    returns (per-launch ms list, wall ms per step) from HIP events."""
-    for i in range(warmup):
-        launches[i % len(launches)]()
-    torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record()
-    for i in range(steps):
-        starts[i].record()
-        launches[i % len(launches)]()
-        ends[i].record()
-    t1.record()
-    torch.cuda.synchronize()
-    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return per, t0.elapsed_time(t1) / steps
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
-def _graph_time(launches, warmup, steps):
-    """Capture ``steps`` launches (``launches[i % len]``) in one HIP graph,
-    the way a serving loop runs its decode steps, replay it once (or more)
-    to warm up, then time exactly one replay = ``steps`` steps, bracketed by
-    synchronisations; returns ms per step."""
+# ------------------------------------------------------------------ timing
+def graph_reps(launches, warmup: int, reps: int, inner: int):
+    """``inner`` steps (``launches[i % n]``, so KV-pool copies rotate inside
+    the graph) captured in one HIP graph, replayed ``warmup`` times untimed,
+    then ``reps`` times, each replay bracketed by HIP events on the current
+    stream (the one the kernels are launched on).  Returns the per-step ms of
+    every replay and the mean per-step ms over the whole timed region
+    (synchronised on both sides)."""
     cur = torch.cuda.current_stream()
     side = torch.cuda.Stream()
     side.wait_stream(cur)
-    with torch.cuda.stream(side):              # warm-up outside capture
+    with torch.cuda.stream(side):              # first launches outside capture
         for f in launches:
             f()
     cur.wait_stream(side)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        for i in range(steps):
+        for i in range(inner):
             launches[i % len(launches)]()
-    for _ in range(max(1, -(-warmup // steps))):
+    for _ in range(max(1, warmup)):
         g.replay()
-    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
     t0.record()
-    g.replay()
+    for s, e in ev:
+        s.record()
+        g.replay()
+        e.record()
     t1.record()
     torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / steps
+    per = [s.elapsed_time(e) / inner for s, e in ev]
+    return per, t0.elapsed_time(t1) / (reps * inner)
 
 
-def _copies(b: workloads.PagedBatch, n: int, dev, on_device: bool):
+def eager_reps(launches, warmup: int, reps: int):
+    """Eager launches from Python (host launch cost included), per-launch
+    HIP events; returns the per-launch ms."""
+    for i in range(warmup):
+        launches[i % len(launches)]()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for i, (s, e) in enumerate(ev):
+        s.record()
+        launches[i % len(launches)]()
+        e.record()
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in ev]
+
+
+def _stats(per, wall):
+    return {"ms_per_step": statistics.median(per), "ms_mean": statistics.mean(per), "ms_min": min(per),
+            "ms_max": max(per), "reps": len(per), "ms_per_step_region_mean": wall}
+
+
+def _traffic(name: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, scaled by a copy-kernel calibration), if a committed summary
+    holds it."""
+    p = os.path.join(ROOT, "profiles", f"traffic_{name}.txt")
+    if not os.path.exists(p):
+        return None
+    for line in open(p):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def roofline_hbm(nbytes: int, ms: float, traffic_name: str):
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": _traffic(traffic_name)}
+
+
+def roofline_mfma(flops: int, ms: float, traffic_name: str):
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": _traffic(traffic_name)}
+
+
+# ------------------------------------------------------------------ GPU legs
+def _copies(b: workloads.PagedBatch, n: int, dev):
     """n independent pools (same lengths, own values and tables) so repeated
-    launches stream HBM rather than the Infinity Cache."""
+    launches stream HBM rather than the 256 MB Infinity Cache."""
     out = []
     for i in range(n):
         c = workloads.PagedBatch(**{k: getattr(b, k) for k in (
             "name", "ctx_lens", "q_lens", "num_q_heads", "num_kv_heads", "head_dim", "block_size",
             "num_blocks", "dtype", "rope_theta", "kv_dtype")})
-        out.append(workloads.materialize(c, dev, values_on_device=on_device, seed=2 + i))
+        out.append(workloads.materialize(c, dev, values_on_device=True, seed=2 + i))
     return out
 
 
-def bench_decode(b, copies, warmup, steps, split, dev, hw=0):
-    bs = _copies(b, copies, dev, on_device=True)
+def bench_paged(b, copies, warmup, reps, inner, dev, split=0, hw=0, eager=True, rope=False):
+    """One paged-attention launch per step over batch ``b`` (decode, mixed or
+    prefill); with ``rope`` q is rotated on load (RoPE table rows c_i + r)."""
+    xs = _copies(b, copies, dev)
+    t = time.perf_counter()
     plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=b.num_q_heads, num_kv_heads=b.num_kv_heads,
                                head_dim=b.head_dim, block_size=b.block_size, dtype=b.dtype, device=dev,
                                split_tokens=split, heads_per_wg=hw)
-    outs = [torch.empty_like(x.q) for x in bs]
-    launches = [lambda x=x, o=o: paged.paged_attention(plan, x.q, x.k_cache, x.v_cache, x.block_table, out=o)
-                for x, o in zip(bs, outs)]
-    per, wall = _events_time(launches, warmup, steps)
-    step = _graph_time(launches, warmup, steps)
-    nbytes = workloads.decode_bytes(b)
-    res = {
-        "bytes_per_launch": nbytes, "flops_per_launch": workloads.attention_flops(b),
-        # graph replay: launches run back to back, so the step time is the
-        # launch's duration on the stream (decode kernel + split merge if any)
-        "ms_per_step": step, "kernel_ms_mean": step,
-        "gbs": nbytes / (step * 1e-3) / 1e9, "kernel_gbs": nbytes / (step * 1e-3) / 1e9,
-        # eager launches from Python, for comparison (host launch cost included)
-        "eager_ms_per_step": wall, "eager_launch_ms_mean": statistics.mean(per),
-        "eager_launch_ms_median": statistics.median(per),
-        "split_tokens": plan.info["split_tokens"], "work_items": plan.info["work_items"],
-        "heads_per_wg": plan.info["heads_per_wg"], "decode_waves": plan.info["decode_waves"],
-        "pool_copies": copies,
-    }
-    res["hbm_frac"] = res["kernel_gbs"] / HBM_PEAK_GBS
-    return res, bs[0], plan
+    torch.cuda.synchronize()
+    plan_ms = (time.perf_counter() - t) * 1e3
+    outs = [torch.empty_like(x.q) for x in xs]
+    launches = [lambda x=x, o=o: paged.paged_attention(plan, x.q, x.k_cache, x.v_cache, x.block_table, out=o,
+                                                       rope=(x.cos, x.sin, "position") if rope else None)
+                for x, o in zip(xs, outs)]
+    per, wall = graph_reps(launches, warmup, reps, inner)
+    res = _stats(per, wall)
+    res.update({"bytes_per_launch": workloads.decode_bytes(b), "flops_per_launch": workloads.attention_flops(b),
+                "graph_steps_per_replay": inner, "pool_copies": copies, "plan_create_upload_ms": plan_ms,
+                **{k: plan.info[k] for k in ("work_items", "split_tokens", "heads_per_wg", "decode_segments")}})
+    if eager:
+        ep = eager_reps(launches, warmup, reps)
+        res["eager_ms_median"] = statistics.median(ep)
+    return res, xs[0], outs[0]
 
 
-def bench_prefill(b, copies, warmup, steps, dev):
-    bs = _copies(b, copies, dev, on_device=True)
-    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=b.num_q_heads, num_kv_heads=b.num_kv_heads,
-                               head_dim=b.head_dim, block_size=b.block_size, dtype=b.dtype, device=dev)
-    outs = [torch.empty_like(x.q) for x in bs]
-    pos = [torch.cat([torch.arange(c, c + q) for c, q in zip(b.ctx_lens, b.q_lens)]).to(dev) for _ in bs]
-
-    def write(x, p):
-        paged.rope_kv_write(x.k_new, x.v_new, x.cos, x.sin, x.k_cache, x.v_cache, x.slot_mapping, rope_rows=p)
-
-    def attn(x, o):
-        paged.paged_attention(plan, x.q, x.k_cache, x.v_cache, x.block_table, out=o, rope=(x.cos, x.sin, "position"))
-
-    wper, _ = _events_time([lambda x=x, p=p: write(x, p) for x, p in zip(bs, pos)], warmup, steps)
-    aper, _ = _events_time([lambda x=x, o=o: attn(x, o) for x, o in zip(bs, outs)], warmup, steps)
-    _, wall = _events_time([lambda x=x, p=p, o=o: (write(x, p), attn(x, o)) for x, p, o in zip(bs, pos, outs)],
-                           warmup, steps)
-    flops = workloads.attention_flops(b)
-    am = statistics.mean(aper)
-    wm = statistics.mean(wper)
-    wb = workloads.rope_write_bytes(b)
-    return {
-        "flops_per_launch": flops, "attn_kernel_ms_mean": am, "tflops": flops / (am * 1e-3) / 1e12,
-        "mfma_frac": flops / (am * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
-        "rope_write_ms_mean": wm, "rope_write_gbs": wb / (wm * 1e-3) / 1e9,
-        "step_ms": wall, "step_tflops": flops / (wall * 1e-3) / 1e12,
-        "tokens": b.rows, "work_items": plan.info["work_items"],
-    }
+def bench_rope_write(b, x, warmup, reps, dev):
+    """The fused RoPE + KV write of the batch's new tokens (graph-timed)."""
+    pos = torch.cat([torch.arange(c, c + q) for c, q in zip(b.ctx_lens, b.q_lens)]).to(dev)
+    f = [lambda: paged.rope_kv_write(x.k_new, x.v_new, x.cos, x.sin, x.k_cache, x.v_cache, x.slot_mapping,
+                                     rope_rows=pos)]
+    per, wall = graph_reps(f, warmup, reps, 4)
+    nb = workloads.rope_write_bytes(b)
+    ms = statistics.median(per)
+    return {"ms_per_step": ms, "bytes": nb, "gbs": nb / (ms * 1e-3) / 1e9, "hbm_frac": nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
-def bench_qkv(n_tokens, hidden, Hq, Hkv, D, weight_copies, warmup, steps, dev, seed=5):
+def bench_qkv(n_tokens, hidden, Hq, Hkv, D, weight_copies, warmup, reps, dev, seed=5):
     """Fused QKV projection + RoPE + KV write (``gllm_qkv_rope_kv_write``) vs
     the unfused path (three bf16 GEMMs through torch/hipBLASLt + the RoPE/KV
     write kernel), both graph-timed.  Weight copies are rotated so a decode
@@ -186,8 +214,9 @@ def bench_qkv(n_tokens, hidden, Hq, Hkv, D, weight_copies, warmup, steps, dev, s
         paged.rope_kv_write(k.view(n_tokens, Hkv, D), v.view(n_tokens, Hkv, D), cos, sin, kc, vc, slots,
                             q=q.view(n_tokens, Hq, D), q_out=q_out, rope_rows=pos)
 
-    tf = _graph_time([lambda w=w: fused(w) for w, _ in ws], warmup, steps)
-    tu = _graph_time([lambda wt=wt: unfused(wt) for _, wt in ws], warmup, steps)
+    inner = weight_copies
+    tf = statistics.median(graph_reps([lambda w=w: fused(w) for w, _ in ws], warmup, reps, inner)[0])
+    tu = statistics.median(graph_reps([lambda wt=wt: unfused(wt) for _, wt in ws], warmup, reps, inner)[0])
     flops = 2 * n_tokens * (Hq + 2 * Hkv) * D * hidden
     wbytes = (Hq + 2 * Hkv) * D * hidden * 2
     iobytes = wbytes + n_tokens * hidden * 2 + n_tokens * (Hq + 2 * Hkv) * D * 2
@@ -197,7 +226,7 @@ def bench_qkv(n_tokens, hidden, Hq, Hkv, D, weight_copies, warmup, steps, dev, s
             "weight_copies": weight_copies}
 
 
-def bench_metadata(b: workloads.PagedBatch, warmup, steps, dev, cpu: bool):
+def bench_metadata(b: workloads.PagedBatch, warmup, reps, dev, cpu: bool):
     """Device metadata builder (query-row slots + positions + cu_seqlens) on
     one batch; with ``cpu`` also the reference path's host builder
     (llm.py:245-293: per-row loop, left-padded slot mapping, dense 0/-inf
@@ -206,14 +235,13 @@ def bench_metadata(b: workloads.PagedBatch, warmup, steps, dev, cpu: bool):
     sl = torch.tensor(b.seq_lens, dtype=torch.int32, device=dev)
     ql = torch.tensor(b.q_lens, dtype=torch.int32, device=dev)
     launches = [lambda: paged.build_metadata(bt, sl, ql, b.block_size, num_rows=b.rows)]
-    step = _graph_time(launches, warmup, steps)
-    res = {"rows": b.rows, "seqs": len(b.q_lens), "gpu_us": step * 1e3}
+    per, _ = graph_reps(launches, warmup, reps, 16)
+    res = {"rows": b.rows, "seqs": len(b.q_lens), "gpu_us": statistics.median(per) * 1e3}
     if cpu:
         from oracle import metadata as om
-        import time
         bt_np = bt.cpu().numpy()
         ts = []
-        for i in range(4):
+        for _ in range(4):
             t0 = time.perf_counter()
             om.build_metadata(b.ctx_lens, b.q_lens, bt_np, b.block_size, dtype=b.dtype)
             ts.append(time.perf_counter() - t0)
@@ -221,18 +249,80 @@ def bench_metadata(b: workloads.PagedBatch, warmup, steps, dev, cpu: bool):
     return res
 
 
-def cpu_baseline_decode(x: workloads.PagedBatch, nbytes: int):
-    """The reference's CPU path for config (b): padded slot mapping + 0/-inf
-    bias (llm.py:245-274), dense gather with the dtype cast (attention.py:
-    165-170), GQA expand + softmax attention (reference_attention.py), fp32."""
-    from oracle import attention as oa
-    from oracle import metadata as om
+# ------------------------------------------------------------------ CPU baseline
+def _cpu_setup():
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    return cores
+
+
+def cpu_baseline_per_sequence(x: workloads.PagedBatch, seqs: list[int], unit: str, what: str):
+    """The reference's CPU path, one sequence at a time (B = 1: no padding),
+    on the batch's own inputs copied from the GPU: per-sequence metadata
+    (llm.py:245-274), dense K/V gather through the slot mapping with the
+    dtype cast (attention.py:165-170), q rotated (attention.py:76-119) when the
+    batch carries a RoPE table, then GQA expand + softmax attention with the
+    0/-inf bias (reference_attention.py:5-51), fp32 torch on every host core.
+    The metadata build is outside the timed region (once per engine step);
+    one untimed warm-up call, then one timed pass over ``seqs``.  Work per
+    sequence uses the same formulas as the GPU figure, so ``value`` is
+    directly comparable."""
+    from oracle import attention as oa
+    from oracle import metadata as om
+    from oracle import rope as orope
+    cores = _cpu_setup()
+    bs, Hkv, D = x.block_size, x.num_kv_heads, x.head_dim
+    rope = x.cos is not None
+    cos_c = x.cos.cpu().float() if rope else None
+    sin_c = x.sin.cpu().float() if rope else None
+    bt_all = x.block_table.cpu()
+    kv_view = lambda t: t.view(-1, bs, Hkv, D)
+    jobs = []
+    for i in seqs:
+        c, q, r0 = x.ctx_lens[i], x.q_lens[i], x.q_row_start[i]
+        L = c + q
+        nb = -(-L // bs)
+        blocks = bt_all[i, :nb].to(torch.int64)
+        kc = kv_view(x.k_cache)[blocks.to(x.k_cache.device)].cpu().reshape(-1, Hkv, D)   # the sequence's pages
+        vc = kv_view(x.v_cache)[blocks.to(x.v_cache.device)].cpu().reshape(-1, Hkv, D)
+        meta = om.build_metadata([c], [q], torch.arange(nb, dtype=torch.int32).numpy()[None], bs, torch.float32)
+        qq = x.q[r0:r0 + q].cpu().float().unsqueeze(0)
+        pos = torch.arange(c, c + q)
+        jobs.append((kc, vc, meta, qq, pos))
+
+    def run(job):
+        kc, vc, meta, qq, pos = job
+        if rope:
+            qq = orope.apply_rope(qq, cos_c[pos].unsqueeze(0), sin_c[pos].unsqueeze(0))
+        k = oa.kv_gather(kc, meta.slot_mapping, torch.float32)
+        v = oa.kv_gather(vc, meta.slot_mapping, torch.float32)
+        return oa.reference_attention(qq, k, v, meta.bias)
+
+    run(jobs[min(range(len(jobs)), key=lambda j: jobs[j][3].shape[1] * jobs[j][0].shape[0])])
+    t = time.perf_counter()
+    for job in jobs:
+        run(job)
+    sec = time.perf_counter() - t
+    sub = workloads.PagedBatch("sample", [x.ctx_lens[i] for i in seqs], [x.q_lens[i] for i in seqs],
+                               x.num_q_heads, Hkv, D, bs, x.num_blocks, x.dtype, kv_dtype=x.kv_dtype)
+    work = workloads.decode_bytes(sub) / 1e9 if unit == "GB/s" else workloads.attention_flops(sub) / 1e12
+    return {"value": work / sec, "unit": unit, "cores": cores, "kind": "port",
+            "sample": f"{what}: {len(seqs)} of {len(x.q_lens)} sequences, one at a time (B=1), "
+                      f"{sec:.2f} s for {work:.4g} {'GB' if unit == 'GB/s' else 'TFLOP'} of the same "
+                      f"formula as the GPU figure; fp32 torch on {cores} threads of {cpu_model()}"}
+
+
+def cpu_baseline_batched(x: workloads.PagedBatch):
+    """Config (b): the reference's CPU path on the whole batch at once, as
+    the engine runs it (padded slot mapping + 0/-inf bias, llm.py:245-274;
+    dense gather, attention.py:165-170; GQA expand + softmax attention,
+    reference_attention.py), fp32; median of 3 after 1 warm-up."""
+    from oracle import attention as oa
+    from oracle import metadata as om
+    cores = _cpu_setup()
     bt = x.block_table.cpu().numpy()
     meta = om.build_metadata(x.ctx_lens, x.q_lens, bt, x.block_size, torch.float32)
-    kc = x.k_cache.cpu()
-    vc = x.v_cache.cpu()
+    kc, vc = x.k_cache.cpu(), x.v_cache.cpu()
     q = x.q.cpu().view(len(x.q_lens), 1, x.num_q_heads, x.head_dim).float()
 
     def run():
@@ -247,30 +337,18 @@ def cpu_baseline_decode(x: workloads.PagedBatch, nbytes: int):
         run()
         ts.append(time.perf_counter() - t)
     med = statistics.median(ts)
-    return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"full config (b) batch, median of 3 after 1 warm-up, {med * 1e3:.1f} ms/batch, "
-                      f"fp32 torch on {platform.processor() or platform.machine()}"}
+    return {"value": workloads.decode_bytes(x) / med / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"full config (b) batch (B=64, padded, as the engine batches it), median of 3 after "
+                      f"1 warm-up, {med * 1e3:.1f} ms/batch; fp32 torch on {cores} threads of {cpu_model()}"}
 
 
-def _traffic(name: str):
-    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, scaled by a copy-kernel calibration), if a committed summary
-    holds it."""
-    p = os.path.join(ROOT, "profiles", f"traffic_{name}.txt")
-    if not os.path.exists(p):
-        return None
-    for line in open(p):
-        if line.startswith("traffic_bytes_per_launch:"):
-            return int(float(line.split(":", 1)[1]))
-    return None
-
-
+# ------------------------------------------------------------------ main
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--steps", type=int, default=60, help="timed steps (graph replays) of the headline config")
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="b,c,d,e")
+    ap.add_argument("--configs", default="d,c,b,e")
     ap.add_argument("--split", type=int, default=0, help="decode split tokens (0 = planner's choice)")
     ap.add_argument("--hw", type=int, default=0, help="kv heads per decode workgroup (0 = planner's choice)")
     ap.add_argument("--copies", type=int, default=4, help="KV pool copies rotated for config (b)")
@@ -279,52 +357,78 @@ def main():
                     help="also run a plain 256 MiB device copy (known bytes) for counter calibration")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only: --gpus must be 1 "
-                                   "(multi-GPU sharding is described in DESIGN.md, not built)"}))
+        print(json.dumps({"error": "this build runs on one GPU only: --gpus must be 1 (how the path would "
+                                   "shard over several GPUs is described in DESIGN.md; nothing multi-GPU is built)"}))
         sys.exit(2)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     cfgs = args.configs.split(",")
+    reps = max(args.steps, 1)
+    cpu = not args.no_cpu
     extra = {}
     head = None
-    if "b" in cfgs:
-        b = workloads.config_b()
-        head, x0, _ = bench_decode(b, args.copies, args.warmup, args.steps, args.split, dev, args.hw)
-        extra["decode_1b"] = head
-        extra["metadata_decode_1b"] = bench_metadata(x0, args.warmup, args.steps, dev, not args.no_cpu)
-        # the same batch over an fp8 (e4m3fn) KV pool: half the K/V bytes
-        b8 = workloads.config_b()
-        b8.kv_dtype = torch.float8_e4m3fn
-        r8, _, _ = bench_decode(b8, args.copies, args.warmup, args.steps, args.split, dev, args.hw)
-        r8["speedup_vs_bf16_kv"] = head["ms_per_step"] / r8["ms_per_step"]
-        extra["decode_1b_fp8kv"] = r8
-        torch.cuda.empty_cache()
-        # fused QKV projection + RoPE + KV write for the same 64 decode tokens (1B layer)
-        extra["qkv_decode_1b"] = bench_qkv(64, 2048, 32, 8, 64, 24, args.warmup, args.steps, dev)
-        torch.cuda.empty_cache()
-    if "c" in cfgs:
-        extra["prefill_8b"] = bench_prefill(workloads.config_c(), 2, args.warmup, args.steps, dev)
-        torch.cuda.empty_cache()
-        # fused QKV projection + RoPE + KV write for config (c)'s tokens (8B layer)
-        extra["qkv_prefill_8b"] = bench_qkv(workloads.config_c().rows, 4096, 32, 8, 128, 2, args.warmup,
-                                            max(5, args.steps // 3), dev)
-        torch.cuda.empty_cache()
+    head_cpu = None
     if "d" in cfgs:
-        r, xd, _ = bench_decode(workloads.config_d(), 1, args.warmup, args.steps, args.split, dev, args.hw)
-        extra["mixed_8b"] = r
-        extra["metadata_mixed_8b"] = bench_metadata(xd, args.warmup, args.steps, dev, False)
+        d = workloads.config_d()
+        head, xd, _ = bench_paged(d, 1, args.warmup, reps, 4, dev, args.split, args.hw)
+        head["roofline"] = roofline_hbm(head["bytes_per_launch"], head["ms_per_step"], "mixed_8b")
+        extra["mixed_8b"] = head
+        extra["metadata_mixed_8b"] = bench_metadata(xd, args.warmup, reps, dev, False)
+        if cpu:
+            head_cpu = cpu_baseline_per_sequence(xd, list(range(len(d.q_lens))), "GB/s", "all of config (d)")
         del xd
         torch.cuda.empty_cache()
         # the decode sequences of the same batch alone: decode at the 8B head shape
-        d = workloads.config_d()
         dd = workloads.PagedBatch("decode_8b", d.ctx_lens[:256], d.q_lens[:256], d.num_q_heads, d.num_kv_heads,
                                   d.head_dim, d.block_size, d.num_blocks, d.dtype, rope_theta=d.rope_theta)
-        r, _, _ = bench_decode(dd, 1, args.warmup, args.steps, args.split, dev, args.hw)
+        r, _, _ = bench_paged(dd, 1, args.warmup, reps, 4, dev, args.split, args.hw, eager=False)
+        r["roofline"] = roofline_hbm(r["bytes_per_launch"], r["ms_per_step"], "decode_8b")
         extra["decode_8b"] = r
         torch.cuda.empty_cache()
+    if "c" in cfgs:
+        c = workloads.config_c()
+        r, xc, _ = bench_paged(c, 2, args.warmup, reps, 4, dev, eager=False, rope=True)
+        r["roofline"] = roofline_mfma(r["flops_per_launch"], r["ms_per_step"], "prefill_8b")
+        r["rope_kv_write"] = bench_rope_write(c, xc, args.warmup, reps, dev)
+        if cpu:
+            r["cpu_baseline"] = cpu_baseline_per_sequence(xc, list(range(len(c.q_lens))), "TFLOP/s",
+                                                          "all of config (c)")
+        extra["prefill_8b"] = r
+        del xc
+        torch.cuda.empty_cache()
+        # fused QKV projection + RoPE + KV write for config (c)'s tokens (8B layer)
+        extra["qkv_prefill_8b"] = bench_qkv(c.rows, 4096, 32, 8, 128, 2, args.warmup, max(10, reps // 3), dev)
+        torch.cuda.empty_cache()
+    if "b" in cfgs:
+        b = workloads.config_b()
+        r, xb, _ = bench_paged(b, args.copies, args.warmup, reps, 2 * args.copies, dev, args.split, args.hw)
+        r["roofline"] = roofline_hbm(r["bytes_per_launch"], r["ms_per_step"], "decode_1b")
+        extra["metadata_decode_1b"] = bench_metadata(xb, args.warmup, reps, dev, cpu)
+        if cpu:
+            r["cpu_baseline"] = cpu_baseline_batched(xb)
+        extra["decode_1b"] = r
+        del xb
+        # the same batch over an fp8 (e4m3fn) KV pool: half the K/V bytes
+        b8 = workloads.config_b()
+        b8.kv_dtype = torch.float8_e4m3fn
+        r8, _, _ = bench_paged(b8, args.copies, args.warmup, reps, 2 * args.copies, dev, args.split, args.hw,
+                               eager=False)
+        r8["roofline"] = roofline_hbm(r8["bytes_per_launch"], r8["ms_per_step"], "decode_1b_fp8kv")
+        r8["speedup_vs_bf16_kv"] = r["ms_per_step"] / r8["ms_per_step"]
+        extra["decode_1b_fp8kv"] = r8
+        torch.cuda.empty_cache()
+        # fused QKV projection + RoPE + KV write for the same 64 decode tokens (1B layer)
+        extra["qkv_decode_1b"] = bench_qkv(64, 2048, 32, 8, 64, 24, args.warmup, max(10, reps // 3), dev)
+        torch.cuda.empty_cache()
     if "e" in cfgs:
-        r, _, _ = bench_decode(workloads.config_e(), 1, args.warmup, max(5, args.steps // 3), args.split, dev, args.hw)
+        e = workloads.config_e()
+        r, xe, _ = bench_paged(e, 1, args.warmup, max(10, reps // 2), 1, dev, args.split, args.hw, eager=False)
+        r["roofline"] = roofline_hbm(r["bytes_per_launch"], r["ms_per_step"], "long_decode_70b")
+        if cpu:
+            r["cpu_baseline"] = cpu_baseline_per_sequence(xe, list(range(0, len(e.q_lens), 8)), "GB/s",
+                                                          "every 8th sequence of config (e)")
         extra["long_decode_70b"] = r
+        del xe
         torch.cuda.empty_cache()
     if args.calibrate:
         src = torch.empty(128 << 20, dtype=torch.bfloat16, device=dev).fill_(1.0)
@@ -332,25 +436,23 @@ def main():
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-    cpu = None
-    if head is not None and not args.no_cpu:
-        cpu = cpu_baseline_decode(x0, head["bytes_per_launch"])
     line = {
         "metric": "decode attn GB/s (% HBM peak); prefill attn TFLOP/s (% MFMA peak), 8B GQA",
-        "value": round(head["gbs"], 2) if head else None,
+        "value": round(head["roofline"]["achieved"], 2) if head else None,
         "unit": "GB/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "n_gpus": 1, "steps": reps, "warmup": args.warmup,
         "ms_per_step": round(head["ms_per_step"], 5) if head else None,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic (seeded N(0,1) Q/K/V, random block tables)",
-        "config": {"workload": "decode paged attention, Llama-3.2-1B heads: B 64, Hq 32 / Hkv 8, D 64, "
-                               "bs 16, seq len U{128..2048}, 16384-block pool, 1 query token per sequence",
-                   "global_batch": 64, "parallelism": "none (1 GPU)",
-                   "launch": "the K timed steps captured in one HIP graph, 4 KV pool copies rotated"},
-        "roofline": None if head is None else {
-            "bound": "hbm", "achieved": round(head["kernel_gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(head["hbm_frac"], 4), "traffic": _traffic("decode_1b")},
-        "cpu_baseline": cpu,
+        "config": {"workload": "config (d): mixed continuous batch, Llama-3.1-8B heads (Hq 32 / Hkv 8, D 128), "
+                               "bs 16: 256 decode sequences with L log-uniform in [256, 8192] + 4 chunked "
+                               "prefills of 512 tokens on contexts U{0..4096}, 131072-block pool, Q/K/V "
+                               "N(0,1); one paged attention launch per step",
+                   "global_batch": 260, "parallelism": "none (1 GPU)",
+                   "timing": "4 steps captured in one HIP graph; per-step time = median over the timed "
+                             "replays (HIP events on the launch stream around each replay) / 4"},
+        "roofline": head["roofline"] if head else None,
+        "cpu_baseline": head_cpu,
         "extra": extra,
     }
     print(json.dumps(line))
