@@ -717,7 +717,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 
   const float sl2 = a.scale * kLog2e;
   float m = kNegInf, lsum = 0.f;
-  float sbase = 0.f;             // value the tile's S accumulators start from
+  float sbase = 0.f;             // dense mode: value the tile's S accumulators start from
   f32x16 o[NO];
 #pragma unroll
   for (int db = 0; db < NO; ++db)
@@ -726,16 +726,64 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 
   // Softmax of one 32-key half, in pieces that the tile loop interleaves
   // with MFMAs: lane holds raw scores S[key k0 + 8(j/4) + 4h + j%4][row n].
-  // sm_max: mask, row max, running-max update (lazy rescale: the max only
-  // moves when a row's max exceeds it by more than 8 in log2 units, so
-  // p <= 2^8; numerator and denominator share m, so the result is exact);
-  // sm_exp: p = 2^(s - m) for 4 scores; sm_sum: row sum; sm_cvt: P as two
-  // bf16 B operands.  Q is pre-scaled by scale * log2(e) and the S
-  // accumulators start at -m (the running max when the tile begins, 0 while
-  // it is -inf), so the MFMA yields s = q.k scale log2(e) - m directly: the
-  // exponent needs no per-score FMA while the max stays put (a subtract of
-  // the max's move otherwise, rare with the lazy rescale).
+  // Q is pre-scaled by scale * log2(e), so scores come out in log2 units.
+  //
+  // Paged (causal) mode: each row keeps a reference r and p = 2^(s - r).  The
+  // first half-tile of the row (keys 0..31; key 0 is visible to every row)
+  // sets r = 0 when its max m1 lies in [-T, T] and r = m1 otherwise, so every
+  // row holds some p >= 2^-T and later tiny p lose nothing.  After that S
+  // accumulates from zero and, while r = 0, p = 2^s directly: no S
+  // initialisation, no running max, no subtraction per score.  The only check
+  // is one compare of each lane's partial sum against 2^T: a lane over it
+  // (some p > 2^T) sends the wave into a rare fix-up that recomputes the
+  // half's S from LDS, moves the reference of every row whose max passed T up
+  // to that max (O and l rescaled by 2^-max, exactly) and recomputes p.  With
+  // T = 64, p <= 2^64 keeps l and O far from fp32 overflow.  Numerator and
+  // denominator share r, so the result is the exact softmax.
+  //
+  // Dense (arbitrary bias) mode: lazy running max (the max only moves when a
+  // row's max exceeds it by more than 8, so p <= 2^8); the S accumulators
+  // start at -m, so the MFMA yields s - m directly (a subtract of the max's
+  // move otherwise, rare).
+  constexpr bool kFast = !DENSE;
+  constexpr float kT = 64.f;
+  constexpr float kTwoT = 18446744073709551616.f;   // 2^64
+  float rref = 0.f;              // paged mode: the row's reference r (log2 units)
+  bool sub = false;              // paged mode, wave-uniform: some row has r != 0
   struct Soft { float alpha, dlt, psum; };
+  auto row_max = [&](const f32x16& s) {
+    float tmax = kNegInf;
+#pragma unroll
+    for (int j = 0; j < 16; j += 2)
+      tmax = __builtin_elementwise_maximum(tmax, __builtin_elementwise_maximum(s[j], s[j + 1]));
+    auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+    return __builtin_elementwise_maximum(__uint_as_float(x[0]), __uint_as_float(x[1]));
+  };
+  auto apply_mask = [&](f32x16& s, int k0) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int key = k0 + 8 * (j >> 2) + 4 * h + (j & 3);
+      s[j] = key > vis ? kNegInf : s[j];
+    }
+  };
+  // paged mode, piece 0: the reference's subtraction (rare), the causal mask,
+  // and on the row's first half-tile the choice of r
+  auto fs_prep = [&](f32x16& s, int k0, bool mask, bool first) {
+    if (sub) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) s[j] -= rref;
+    }
+    if (mask) apply_mask(s, k0);
+    if (first) {
+      const float m1 = row_max(s);
+      rref = (m1 >= -kT && m1 <= kT) || m1 == kNegInf ? 0.f : m1;
+      sub = __builtin_amdgcn_ballot_w64(rref != 0.f) != 0;
+      if (sub) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s[j] -= rref;
+      }
+    }
+  };
   auto sm_max = [&](f32x16& s, int k0, bool mask, Soft& q) {
     if (DENSE) {
       const __bf16* bp = (const __bf16*)a.bias + (int64_t)seq * a.bias_batch_stride + (int64_t)rr * a.bias_row_stride;
@@ -746,20 +794,9 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
         s[j] = __builtin_fmaf(bv, kLog2e, s[j]);
       }
     } else if (mask) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int key = k0 + 8 * (j >> 2) + 4 * h + (j & 3);
-        s[j] = key > vis ? kNegInf : s[j];
-      }
+      apply_mask(s, k0);
     }
-    float tmax = kNegInf;
-#pragma unroll
-    for (int j = 0; j < 16; j += 2)
-      tmax = __builtin_elementwise_maximum(tmax, __builtin_elementwise_maximum(s[j], s[j + 1]));
-    {
-      auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
-      tmax = __builtin_elementwise_maximum(__uint_as_float(x[0]), __uint_as_float(x[1])) - sbase;
-    }
+    const float tmax = row_max(s) - sbase;
     const float mn = tmax > m + 8.f ? tmax : m;
     q.alpha = mn > m ? fast_exp2(m - mn) : 1.f;
     m = mn;
@@ -779,7 +816,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 #pragma unroll
     for (int e = 0; e < 4; ++e) ps4[e] = (s[e] + s[e + 4]) + (s[e + 8] + s[e + 12]);
     q.psum = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
-    lsum = __builtin_fmaf(lsum, q.alpha, q.psum);
+    if (!kFast) lsum = __builtin_fmaf(lsum, q.alpha, q.psum);
   };
   auto sm_cvt = [&](const f32x16& s, bf16x8* pb) {
     float pv[8];
@@ -790,20 +827,54 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
     for (int e = 0; e < 8; ++e) pv[e] = s[8 + e];
     pb[1] = to_bf16x8(pv);
   };
-  // Logical softmax piece p (0..7) of a half: max, 4 x exp, sum, convert.
-  auto sm_piece = [&](int p, f32x16& s, int k0, bool mask, Soft& q, bf16x8* pb) {
-    if (p == 0) sm_max(s, k0, mask, q);
+  // Logical softmax piece p (0..7) of a half: max (dense) or prep (paged),
+  // 4 x exp, sum, convert.
+  auto sm_piece = [&](int p, f32x16& s, int k0, bool mask, Soft& q, bf16x8* pb, bool first) {
+    if (p == 0) {
+      if (kFast) fs_prep(s, k0, mask, first);
+      else sm_max(s, k0, mask, q);
+    }
     else if (p <= 4) sm_exp(s, 4 * (p - 1));
     else if (p == 5) sm_sum(s, q);
     else if (p == 6) sm_cvt(s, pb);
   };
-  // q.psum >= 0 always; testing it keeps the half's exponentials ahead of the
-  // branch, in the region where they overlap the MFMAs.
-  auto rescale = [&](const Soft& q) {
-    if (__builtin_amdgcn_ballot_w64(q.alpha != 1.f || q.psum < 0.f)) {
+  // After a half's pieces.  Dense: the rare O rescale of the lazy max
+  // (q.psum >= 0 always; testing it keeps the half's exponentials ahead of
+  // the branch, in the region where they overlap the MFMAs).  Paged: the rare
+  // fix-up of a half whose p passed 2^T (S recomputed from the stage `st`,
+  // half kb), then the half's sum joins the row's.
+  auto commit = [&](Soft& q, const char* st, int kb, int k0, bool mask, bf16x8* pb) {
+    if (!kFast) {
+      if (__builtin_amdgcn_ballot_w64(q.alpha != 1.f || q.psum < 0.f)) {
 #pragma unroll
-      for (int db = 0; db < NO; ++db) o[db] *= q.alpha;
+        for (int db = 0; db < NO; ++db) o[db] *= q.alpha;
+      }
+      return;
     }
+    if (__builtin_amdgcn_ballot_w64(q.psum > kTwoT)) {
+      f32x16 t = {};
+#pragma unroll
+      for (int kk = 0; kk < NQ; ++kk)
+        t = mfma32(as_bf16x8(*reinterpret_cast<const u32x4*>(st + 32 * kb * RW + koff[kk])), qB[kk], t);
+      if (sub) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) t[j] -= rref;
+      }
+      if (mask) apply_mask(t, k0);
+      const float tmax = row_max(t);
+      const float d = tmax > kT ? tmax : 0.f;          // rows whose p passed 2^T move up to their max
+      const float alpha = fast_exp2(-d);
+#pragma unroll
+      for (int db = 0; db < NO; ++db) o[db] *= alpha;
+      lsum *= alpha;
+      rref += d;
+      sub = __builtin_amdgcn_ballot_w64(rref != 0.f) != 0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) t[j] = fast_exp2(t[j] - d);
+      sm_sum(t, q);
+      sm_cvt(t, pb);
+    }
+    lsum += q.psum;
   };
   // V^T operand reads of one 16-key group (tp) and output block (db) of half kb
   auto vread1 = [&](const char* st, int kb, int tp, int db) -> u32x4 {
@@ -820,8 +891,10 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   // 0 and one softmax piece of half 0; (2) the MFMAs of O^T += V^T P^T half 0,
   // each followed by V reads and a softmax piece of half 1; (3) P V of half 1.
   // One wave thus keeps the matrix core busy while its own VALU work runs;
-  // the two rescales of O (rare, wave-uniform branches) split the regions.
-  auto compute = [&](const char* st, int ts, bool mask, bool dma, int dts, int dstage, const uint32_t (&blk)[CHD]) {
+  // the two commits (rare wave-uniform branches inside) split the regions.
+  // `first`: the row's first tile (key 0).
+  auto compute = [&](const char* st, int ts, bool mask, bool dma, int dts, int dstage, const uint32_t (&blk)[CHD],
+                     bool first) {
     f32x16 s0, s1;
     u32x4 va0[2][NO], va1[2][NO];
     bf16x8 pb0[2], pb1[2];
@@ -829,9 +902,14 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
     u32x4 ka[2][NQ];
 #pragma unroll
     for (int kk = 0; kk < NQ; ++kk) ka[0][kk] = *reinterpret_cast<const u32x4*>(st + koff[kk]);
-    sbase = m == kNegInf ? 0.f : -m;     // both halves start from the max before this tile
+    if (kFast) {
+      s0 = f32x16{};
+      s1 = f32x16{};
+    } else {
+      sbase = m == kNegInf ? 0.f : -m;     // both halves start from the max before this tile
 #pragma unroll
-    for (int j = 0; j < 16; ++j) s0[j] = sbase, s1[j] = sbase;
+      for (int j = 0; j < 16; ++j) s0[j] = sbase, s1[j] = sbase;
+    }
     // K of half 1 is read between the MFMAs of half 0: the eight waves' reads
     // after a barrier do not all hit LDS at once, and fewer registers are live
 #pragma unroll
@@ -852,10 +930,10 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int p = kk * 8 / NQ; p < (kk + 1) * 8 / NQ; ++p) sm_piece(p, s0, ts, mask, q0, pb0);
+      for (int p = kk * 8 / NQ; p < (kk + 1) * 8 / NQ; ++p) sm_piece(p, s0, ts, mask, q0, pb0, first);
       __builtin_amdgcn_sched_barrier(0);
     }
-    rescale(q0);
+    commit(q0, st, 0, ts, mask, pb0);
     // region 2: P V half 0 | V reads half 1 | softmax half 1
 #pragma unroll
     for (int i = 0; i < 2 * NO; ++i) {
@@ -864,10 +942,11 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
       va1[tp][db] = vread1(st, 1, tp, db);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int p = i * 8 / (2 * NO); p < (i + 1) * 8 / (2 * NO); ++p) sm_piece(p, s1, ts + 32, mask, q1, pb1);
+      for (int p = i * 8 / (2 * NO); p < (i + 1) * 8 / (2 * NO); ++p)
+        sm_piece(p, s1, ts + 32, mask, q1, pb1, false);
       __builtin_amdgcn_sched_barrier(0);
     }
-    rescale(q1);
+    commit(q1, st, 1, ts + 32, mask, pb1);
     // region 3: P V half 1, with the copy of a later tile spread between
     // the MFMAs (a burst of copies right after the barrier stalls the wave)
     static_assert(CHD <= NO, "copy instructions must fit between the P V MFMAs");
@@ -974,9 +1053,9 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
         if (wact && ts < kend_w) {
           const char* st = lds + (t % NS) * Cfg::kStage;
           if (DENSE || ts + BN - 1 > full_end)
-            compute(st, ts, true, dma, dts, dstage, nbid);
+            compute(st, ts, true, dma, dts, dstage, nbid, t == 0);
           else
-            compute(st, ts, false, dma, dts, dstage, nbid);
+            compute(st, ts, false, dma, dts, dstage, nbid, t == 0);
         } else if (dma) {
           dma_issue(dts, dstage, nbid);
         }

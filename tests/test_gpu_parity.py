@@ -160,6 +160,52 @@ def test_prefill_parity(Hq, Hkv, D):
     assert_close_bf16(out, oracle_paged(b), "prefill")
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_prefill_extreme_scores(D):
+    """Scores far outside the softmax fast path's range [-64, 64] (log2
+    units): q scaled up (most half-tiles overflow 2^64 and take the fix-up),
+    and a first half-tile far below every later key (the row's reference
+    starts at that max, later tiles move it up).  With scores this peaked a
+    handful of keys carry each row, so the bf16 rounding of P no longer
+    averages out: max-abs is held to 4e-2 here (mean-abs to the usual 2e-3);
+    a wrong rescale would be off by O(1)."""
+    print(f"prefill extreme scores D={D}", flush=True)
+    Hq, Hkv = 32, 8
+    # the kernel rounds q * scale * log2(e) to bf16 once; at these magnitudes
+    # that rounding alone moves scores by ~0.3, so the oracle gets the same
+    # effective q (the softmax logic is what is under test here)
+    sl2 = torch.tensor(1.0 / math.sqrt(D), dtype=torch.float32) * torch.tensor(1.4426950408889634,
+                                                                                  dtype=torch.float32)
+
+    def q_eff(q):
+        return (q.float().cpu() * sl2).to(torch.bfloat16).float() / sl2
+
+    b = make_batch([0, 0, 100], [200, 70, 90], Hq, Hkv, D)
+    b.q.mul_(30.0)                                          # s ~ N(0, (30 * 1.44)^2): row maxima > 64
+    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D,
+                               block_size=16, dtype=torch.bfloat16, device=DEV)
+    out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
+    torch.cuda.synchronize()
+    assert_close_bf16(out, oracle_paged(b, q_eff(b.q)), "prefill, scaled q", max_abs=4e-2)
+    # every query row = u; keys 0..31 of each sequence = -6 u / |u| * sqrt(D): first half-tile
+    # scores ~ -6 sqrt(D) * 1.44 < -64, later keys N(0, 1) scores
+    g = torch.Generator().manual_seed(7)
+    c = make_batch([0, 40], [100, 60], Hq, Hkv, D)
+    u = torch.randn(D, generator=g)
+    u = u / u.norm() * D ** 0.5
+    c.q.copy_(u.to(c.q.dtype).expand_as(c.q))
+    bt = c.block_table.cpu()
+    for i in range(2):
+        for p in range(32):
+            slot = int(bt[i, p // 16]) * 16 + p % 16
+            c.k_cache[slot] = (-6.0 * u).to(c.k_cache.dtype).to(DEV)
+    plan = paged.AttentionPlan(c.q_lens, c.seq_lens, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D,
+                               block_size=16, dtype=torch.bfloat16, device=DEV)
+    out = paged.paged_attention(plan, c.q, c.k_cache, c.v_cache, c.block_table)
+    torch.cuda.synchronize()
+    assert_close_bf16(out, oracle_paged(c, q_eff(c.q)), "prefill, very negative first tile", max_abs=4e-2)
+
+
 def test_prefill_rope_in_kernel_matches_prerotated():
     """RoPE fused into the attention kernel's q load == RoPE applied first."""
     print("prefill rope fused", flush=True)
