@@ -507,14 +507,20 @@ __global__ void __launch_bounds__(64) merge_splits_kernel(AttnArgs a) {
 }
 
 // ============================================================== prefill
+// LDS ring of NS stages: the K tiles of all stages first, then the V tiles
+// ([K_0 .. K_{NS-1}][V_0 .. V_{NS-1}]), so that with the stage known at
+// compile time every operand read is one per-lane register plus an immediate
+// offset (< 64 KB): K reads need no base at all, V reads one base register
+// that holds the V region's start.
 template <int D, int NS> struct PrefillCfg {
   static constexpr int kBN = 64;                   // keys per tile
   static constexpr int kRow = D * 2;               // bytes per K/V row in LDS (16-byte chunks XOR-swizzled)
   static constexpr int kTile = kBN * kRow;         // bytes per K (or V) tile
-  static constexpr int kStage = 2 * kTile;         // one pipeline stage: K tile, then V tile
   static constexpr int kStages = NS;               // LDS ring: tiles t+1 .. t+NS-1 in flight while t is computed
+  static constexpr int kVBase = NS * kTile;        // start of the V tiles
   static constexpr int kBidCache = 1024;           // block ids cached per workgroup
-  static constexpr int kLdsBytes = kStages * kStage + kBidCache * 4;
+  static constexpr int kLdsBytes = 2 * NS * kTile + kBidCache * 4;
+  static_assert((NS - 1) * kTile + (kBN - 16) * kRow < 65536, "stage offsets must fit a DS immediate");
 };
 
 
@@ -553,7 +559,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   constexpr int RW = Cfg::kRow;
   constexpr int CPR = D / 8;               // 16-byte chunks per key row
   constexpr int NT = 64 * NW;              // threads per workgroup
-  int32_t* const lbid = reinterpret_cast<int32_t*>(lds + Cfg::kStages * Cfg::kStage);
+  int32_t* const lbid = reinterpret_cast<int32_t*>(lds + 2 * Cfg::kStages * Cfg::kTile);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n = lane & 31, h = lane >> 5;
 
@@ -631,8 +637,14 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
     for (int r2 = 0; r2 < 2; ++r2) {
       const int row = 4 * h + (i16 >> 2) + 8 * r2;
 #pragma unroll
-      for (int db = 0; db < NO; ++db)
-        voff[r2][db] = Cfg::kTile + row * RW + (((4 * db + clo) ^ pf_swz<D>(row)) << 4) + 8 * (i16 & 1);
+      for (int db = 0; db < NO; ++db) {
+        // the V region's start rides in the register (kept opaque so the
+        // compiler does not move it into the immediate, where it cannot fit
+        // beside the stage offset)
+        int v = Cfg::kVBase + row * RW + (((4 * db + clo) ^ pf_swz<D>(row)) << 4) + 8 * (i16 & 1);
+        asm volatile("" : "+v"(v));
+        voff[r2][db] = v;
+      }
     }
   }
 
@@ -687,7 +699,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   // widened to bf16 when written (`fp8_put`), so LDS always holds bf16.
   auto dma_one = [&](int ts, int stage, const uint32_t (&blk)[CHD], int i, int v) {
     const int sg = i * NW + wave;
-    const uint32_t dst = __builtin_amdgcn_readfirstlane(lds0 + stage * Cfg::kStage + v * Cfg::kTile + sg * 1024);
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(lds0 + v * Cfg::kVBase + stage * Cfg::kTile + sg * 1024);
     lds_dma16(copy_src(ts, blk, i, v), dst);
   };
   u32x2 f8st[CHD][2];                      // fp8 cache: fetched chunks of the tile being copied
@@ -699,7 +711,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   };
   auto fp8_put = [&](int stage, int i, int v) {
     const int sg = i * NW + wave;
-    *reinterpret_cast<u32x4*>(lds + stage * Cfg::kStage + v * Cfg::kTile + sg * 1024 + lane * 16) =
+    *reinterpret_cast<u32x4*>(lds + v * Cfg::kVBase + stage * Cfg::kTile + sg * 1024 + lane * 16) =
         fp8x8_to_bf16x8(f8st[i][v][0], f8st[i][v][1]);
   };
   auto dma_issue = [&](int ts, int stage, const uint32_t (&blk)[CHD]) {
@@ -759,12 +771,13 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
     auto x = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
     return __builtin_elementwise_maximum(__uint_as_float(x[0]), __uint_as_float(x[1]));
   };
+  // key k0 + 8(j/4) + 4h + j%4 is hidden iff 8(j/4) + j%4 > vis - k0 - 4h:
+  // one per-lane limit against compile-time offsets (nothing to hoist onto the
+  // common path)
   auto apply_mask = [&](f32x16& s, int k0) {
+    const int lim = vis - k0 - 4 * h;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int key = k0 + 8 * (j >> 2) + 4 * h + (j & 3);
-      s[j] = key > vis ? kNegInf : s[j];
-    }
+    for (int j = 0; j < 16; ++j) s[j] = 8 * (j >> 2) + (j & 3) > lim ? kNegInf : s[j];
   };
   // paged mode, piece 0: the reference's subtraction (rare), the causal mask,
   // and on the row's first half-tile the choice of r
@@ -876,7 +889,9 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
     }
     lsum += q.psum;
   };
-  // V^T operand reads of one 16-key group (tp) and output block (db) of half kb
+  // V^T operand reads of one 16-key group (tp) and output block (db) of half
+  // kb; st: the stage's K tile (the V tile sits at the same offset from the V
+  // region's start, which voff carries)
   auto vread1 = [&](const char* st, int kb, int tp, int db) -> u32x4 {
     const char* base = st + (32 * kb + 16 * tp) * RW;
     const u32x2 r1 = lds_read_tr16(base + voff[0][db]);
@@ -884,7 +899,8 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
     return u32x4{r1[0], r1[1], r2[0], r2[1]};
   };
 
-  // st: the tile's stage (K at +0, V at +kTile).  The tile is scheduled by
+  // st: the tile's stage (its K tile; V at the same offset in the V region).
+  // The tile is scheduled by
   // hand (sched_barrier fences keep the source order): (1) K reads of half 0,
   // S^T of half 0 with the K reads of half 1 between its MFMAs, then the
   // MFMAs of S^T half 1 each followed by two V reads of half
@@ -1039,27 +1055,32 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   if (!DENSE) __syncthreads();  // block ids in LDS visible
   if (TPB < ntiles) dma_bids(TPB * BN, nbid);
 
-  for (int t0 = 0; t0 < ntiles; t0 += TPB) {
-    wait_vmcnt<0>();                       // this thread's copies of tiles t0 .. t0+TPB-1
-    __syncthreads();
+  // The loop walks the ring NS tiles at a time so that every stage index is a
+  // compile-time constant (operand reads then carry it as an immediate); a
+  // barrier opens each group of TPB tiles.
+  for (int t0 = 0; t0 < ntiles; t0 += NS) {
 #pragma unroll
-    for (int u = 0; u < TPB; ++u) {
-      const int t = t0 + u;
-      if (t < ntiles) {
-        const int ts = t * BN;
-        const bool dma = t + TPB < ntiles;
-        const int dts = (t + TPB) * BN, dstage = (t + TPB) % NS;
-        if (KV8 && dma && wact && ts < kend_w) fp8_fetch(dts, nbid);   // written in the tile's last region
-        if (wact && ts < kend_w) {
-          const char* st = lds + (t % NS) * Cfg::kStage;
-          if (DENSE || ts + BN - 1 > full_end)
-            compute(st, ts, true, dma, dts, dstage, nbid, t == 0);
-          else
-            compute(st, ts, false, dma, dts, dstage, nbid, t == 0);
-        } else if (dma) {
-          dma_issue(dts, dstage, nbid);
+    for (int gi = 0; gi < NS / TPB; ++gi) {
+      const int tg = t0 + gi * TPB;
+      if (tg < ntiles) {
+        wait_vmcnt<0>();                     // this thread's copies of tiles tg .. tg+TPB-1
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < TPB; ++u) {
+          const int t = tg + u;
+          const int stage = gi * TPB + u;    // == t % NS
+          if (t < ntiles) {
+            const int ts = t * BN;
+            const bool dma = t + TPB < ntiles;
+            const int dts = (t + TPB) * BN, dstage = (stage + TPB) % NS;
+            if (KV8 && dma && wact && ts < kend_w) fp8_fetch(dts, nbid);   // written in the tile's last region
+            if (wact && ts < kend_w)
+              compute(lds + stage * Cfg::kTile, ts, DENSE || ts + BN - 1 > full_end, dma, dts, dstage, nbid, t == 0);
+            else if (dma)
+              dma_issue(dts, dstage, nbid);
+            if (t + TPB + 1 < ntiles) dma_bids((t + TPB + 1) * BN, nbid);
+          }
         }
-        if (t + TPB + 1 < ntiles) dma_bids((t + TPB + 1) * BN, nbid);
       }
     }
   }
@@ -1134,12 +1155,16 @@ decode_balanced_kernel(AttnArgs a) {
   }
 }
 
-// Prefill items only.
-template <int D, bool KV8>
-__global__ void __launch_bounds__(64 * kWaves) prefill_bf16_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) char lds[PrefillCfg<D, kPrefillStages>::kLdsBytes];
+// Prefill items only.  NW = 8: one workgroup per CU, a 4-stage ring; NW = 4:
+// two workgroups per CU (one wave per SIMD each), a 2-stage ring, so one
+// workgroup's prologue overlaps the other's main loop.
+template <int D, bool KV8, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
+prefill_bf16_kernel(AttnArgs a) {
+  constexpr int NS = NW == 8 ? kPrefillStages : 2;
+  __shared__ __attribute__((aligned(16))) char lds[PrefillCfg<D, NS>::kLdsBytes];
   const WorkItem it = a.items[blockIdx.x];
-  prefill_wg<D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
+  prefill_wg<D, false, NW, NS, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
 }
 
 template <int D>
@@ -1160,7 +1185,10 @@ static void launch_paged_hk(const AttnArgs& a, bool pf, bool dc, hipStream_t st)
     if constexpr (HW * KW == kWaves)
       hipLaunchKernelGGL((paged_attn_bf16_kernel<D, true, true, HW, KW, KV8>), grid, dim3(64 * kWaves), 0, st, a);
   } else if (pf) {
-    hipLaunchKernelGGL((prefill_bf16_kernel<D, KV8>), grid, dim3(64 * kWaves), 0, st, a);
+    if (a.prefill_waves == 4)
+      hipLaunchKernelGGL((prefill_bf16_kernel<D, KV8, 4>), grid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((prefill_bf16_kernel<D, KV8, kWaves>), grid, dim3(64 * kWaves), 0, st, a);
   } else {
     hipLaunchKernelGGL((paged_attn_bf16_kernel<D, false, true, HW, KW, KV8>), grid, dim3(64 * HW * KW), 0, st, a);
   }
@@ -1186,7 +1214,8 @@ static hipError_t launch_paged_d(const AttnArgs& a, bool pf, bool dc, hipStream_
     if (pf || nw != kWaves) return hipErrorInvalidValue;
     return launch_decode_balanced<D, KV8>(a, st);
   }
-  if (pf && (a.prefill_waves != kWaves || (dc && nw != kWaves))) return hipErrorInvalidValue;
+  if (pf && ((a.prefill_waves != kWaves && (dc || a.prefill_waves != 4)) || (dc && nw != kWaves)))
+    return hipErrorInvalidValue;
   if (nw == 8) {
     switch (hw) {
       case 1: launch_paged_hk<D, 1, 8, KV8>(a, pf, dc, st); break;
