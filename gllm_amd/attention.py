@@ -24,7 +24,9 @@ from . import paged
 @dataclass
 class AttentionMetadata:
     """Field-for-field ``attention.py:12-26`` plus the pool's ``block_size``
-    (the reference keeps it in ``GeneratorParams``; default 16)."""
+    (the reference keeps it in ``GeneratorParams``, ``generator_params.py``).
+    ``block_size=None`` (and the reference's own metadata object, which has
+    no such field) makes :func:`plan_for` derive it from the slot mapping."""
 
     query_lens: torch.Tensor            # [B] int32
     seq_lens: torch.Tensor              # [B] int32
@@ -33,20 +35,51 @@ class AttentionMetadata:
     slot_mapping: torch.Tensor          # [B, T] int64 (unused by the kernels)
     query_slot_mapping: torch.Tensor    # [B, T_q] int64
     bias: torch.Tensor | None           # [B, T_q, T] (unused by the kernels)
-    block_size: int = 16
+    block_size: int | None = None
 
 
-def plan_for(meta: AttentionMetadata, *, num_q_heads: int, num_kv_heads: int, head_dim: int,
+def _block_size(meta, ql: list[int], sl: list[int]) -> int:
+    """The pool's block size, checked against the metadata itself: the first
+    and the last real query row of the longest sequence must sit at
+    ``block_table[i][p // bs] * bs + p % bs`` (``llm.py:245-247,277``).  A
+    given ``block_size`` that disagrees raises; without one, the unique size
+    in 1..1024 that reproduces both slots is taken."""
+    i = max(range(len(sl)), key=lambda j: sl[j])
+    rows = [0, ql[i] - 1]
+    ctx = sl[i] - ql[i]
+    slots = [int(x) for x in meta.query_slot_mapping[i, rows].tolist()]
+    bt = meta.block_table[i].tolist()
+    pos = [ctx + r for r in rows]
+
+    def fits(bs):
+        return all(p // bs < len(bt) and bt[p // bs] * bs + p % bs == s for p, s in zip(pos, slots))
+
+    given = getattr(meta, "block_size", None)
+    if given is not None:
+        if not fits(int(given)):
+            raise ValueError(f"block_size {given} does not match the slot mapping (sequence {i}, rows {rows})")
+        return int(given)
+    cands = [bs for bs in range(1, 1025) if fits(bs)]
+    if len(cands) != 1:
+        raise ValueError(f"cannot derive the block size from the slot mapping ({len(cands)} candidates); "
+                         "set AttentionMetadata.block_size")
+    return cands[0]
+
+
+def plan_for(meta, *, num_q_heads: int, num_kv_heads: int, head_dim: int,
              dtype: torch.dtype, device) -> paged.AttentionPlan:
     """The batch plan, built once per metadata object (one engine step) and
     reused by every layer.  Reads the lengths back once, like the reference's
-    own ``.tolist()`` / ``.item()`` calls in ``llm.py:166,176``."""
+    own ``.tolist()`` / ``.item()`` calls in ``llm.py:166,176``.  ``meta`` is
+    this module's :class:`AttentionMetadata` or the reference's (no
+    ``block_size``: derived from the slot mapping)."""
     plan = getattr(meta, "_gllm_plan", None)
     if plan is None:
         ql = meta.query_lens.tolist()
         sl = meta.seq_lens.tolist()
+        bs = _block_size(meta, ql, sl)
         plan = paged.AttentionPlan(ql, sl, num_q_heads=num_q_heads, num_kv_heads=num_kv_heads,
-                                   head_dim=head_dim, block_size=meta.block_size, dtype=dtype,
+                                   head_dim=head_dim, block_size=bs, dtype=dtype,
                                    device=device, q_seq_stride=meta.query_slot_mapping.shape[1])
         object.__setattr__(meta, "_gllm_plan", plan)
     return plan

@@ -18,14 +18,21 @@ Pinning status (what each function is checked against, in
   mask-equivalence theorem (bias == 0  <=>  p <= c_i + r on real rows).
 * ``rope.rope_cache`` — fp64 closed form, exact identity at position 0.
 * ``rope.apply_rope`` — exact identity at position 0, known-angle rotations,
-  pair-norm preservation, inverse rotation, and an fp64 closed form.
+  pair-norm preservation, inverse rotation, an fp64 closed form, and bit for
+  bit a numpy brute force that rounds to bf16 (round-to-nearest-even, from
+  the bit pattern) after every op, on inputs where one rounding of the exact
+  result differs; in fp32, separate roundings with no fused multiply-add.
 * ``attention.reference_attention`` — fp64 brute-force textbook softmax, one
   visible key => that V row, Q = 0 => mean of visible V, GQA head mapping
   h -> h // G, NaN on fully masked rows.
 * ``attention.attention_layer_forward`` — write-then-gather round trip on a
   sentinel pool, and equality with ``paged_attention`` on real rows.
 * ``attention.paged_attention`` — fp64 brute force, LSE split-merge identity.
-* ``engine`` — RMSNorm / SiLU-MLP closed forms; greedy sampling is argmax.
+* ``engine.rms_norm`` / ``engine.mlp`` — properties fixed by the maths:
+  unit RMS, scale invariance, the one-hot closed form; ``x * silu(x)`` at
+  known values of silu with identity weights, linearity in ``down``.
+* ``engine`` (the layer loop) — the paged engine against a cache-free full
+  recompute; greedy sampling is argmax.
 
 The reference ships no golden vectors or fixtures for this path, so no
 function here is checked against reference-produced numbers; none is left

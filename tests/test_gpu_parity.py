@@ -378,6 +378,76 @@ def test_attention_forward_dropin(dtype):
             assert_close_bf16(out[i, :ql[i]], ref[i, :ql[i]], f"drop-in seq {i}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_attention_layer_forward_real_weights(dtype):
+    """gllm_amd.Attention.forward (projections, RoPE, KV write, attention,
+    linear_o) == attention.py:122-182 restated by the oracle, on random
+    weights; the metadata is the reference's own shape (no block_size: the
+    drop-in derives it from the slot mapping)."""
+    print(f"attention forward {dtype}", flush=True)
+    from dataclasses import dataclass
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(23)
+    Hq, Hkv, D, bs, nb = 16, 4, 64, 8, 96
+    hidden = Hq * D
+    ctx, ql = [0, 40, 9], [17, 1, 1]
+    bt = om.random_block_tables([c + x for c, x in zip(ctx, ql)], bs, nb, g, width=12)
+    meta = om.build_metadata(ctx, ql, bt, bs, dtype)
+    B, Tq = meta.query_slot_mapping.shape
+    x = (torch.randn(B, Tq, hidden, generator=g) * 0.5).to(dtype)
+    names = {n: f"model.layers.3.self_attn.{n}_proj.weight" for n in "qkvo"}
+    w = {names["q"]: torch.randn(Hq * D, hidden, generator=g) / hidden ** 0.5,
+         names["k"]: torch.randn(Hkv * D, hidden, generator=g) / hidden ** 0.5,
+         names["v"]: torch.randn(Hkv * D, hidden, generator=g) / hidden ** 0.5,
+         names["o"]: torch.randn(hidden, Hq * D, generator=g) / hidden ** 0.5}
+    cos_t, sin_t = orope.rope_cache(128, D, 500000.0, dtype)
+    cos, sin = cos_t[meta.positions], sin_t[meta.positions]
+    kv = torch.randn(2, nb * bs, Hkv, D, generator=g).to(dtype)
+    kv_ref = kv.clone()
+    wq, wk, wv, wo = (w[names[n]].to(dtype) for n in "qkvo")
+    # the projections as the drop-in computes them (F.linear on the device), so
+    # the RoPE + KV write below can be compared bit for bit
+    xd = x.to(DEV)
+    q = F.linear(xd, wq.to(DEV)).view(B, Tq, Hq, D).cpu()
+    k = F.linear(xd, wk.to(DEV)).view(B, Tq, Hkv, D).cpu()
+    v = F.linear(xd, wv.to(DEV)).view(B, Tq, Hkv, D).cpu()
+    att_ref, _, _ = oa.attention_layer_forward(q, k, v, cos, sin, kv_ref[0], kv_ref[1], meta,
+                                               sdpa_dtype=torch.float32)
+    ref = F.linear(att_ref.to(dtype).view(B, Tq, -1).float(), wo.float())
+
+    class Cfg:
+        num_attn_heads, num_kv_heads, head_dim, hidden_size = Hq, Hkv, D, hidden
+
+    Cfg.dtype = dtype
+
+    @dataclass
+    class RefMeta:            # attention.py:12-26, field for field, no block_size
+        query_lens: torch.Tensor
+        seq_lens: torch.Tensor
+        max_seq_len: int
+        block_table: torch.Tensor
+        slot_mapping: torch.Tensor
+        query_slot_mapping: torch.Tensor
+        bias: torch.Tensor
+
+    gm = RefMeta(meta.query_lens.to(DEV), meta.seq_lens.to(DEV), meta.max_seq_len, meta.block_table.to(DEV),
+                 meta.slot_mapping.to(DEV), meta.query_slot_mapping.to(DEV), meta.bias.to(DEV))
+    att = gllm_amd.Attention(3, Cfg, w)
+    kvd = kv.to(DEV)
+    out = att.forward(x.to(DEV), cos.to(DEV), sin.to(DEV), kvd, gm).float().cpu()
+    assert gm._gllm_plan.block_size == bs
+    # K/V written bit-exact outside the dummy block
+    assert torch.equal(_bits(kvd)[:, bs:], _bits(kv_ref)[:, bs:])
+    tol = 1e-3 if dtype == torch.float32 else 3e-2
+    for i in range(B):
+        d = (out[i, :ql[i]] - ref[i, :ql[i]]).abs()
+        assert d.max().item() < tol, (i, d.max().item())
+    # Attention.apply_rope: both tensors bit-identical to attention.py:76-119
+    qr, kr = att.apply_rope(q.to(DEV), k.to(DEV), cos.to(DEV), sin.to(DEV))
+    assert torch.equal(_bits(qr), _bits(orope.apply_rope(q, cos, sin)))
+    assert torch.equal(_bits(kr), _bits(orope.apply_rope(k, cos, sin)))
+
+
 # ------------------------------------------------------------ errors
 def test_errors_are_raised():
     print("errors", flush=True)

@@ -7,7 +7,8 @@ Each case draws head counts, head dim, block size, cache dtype and a batch
 that mixes decode rows (one query row, contexts from 0 up to a few thousand
 keys, block-size boundaries included) with prefill rows (chunks on top of
 contexts), so the planners see shapes the hand-written tests do not: ragged
-row blocks, G = 1 .. 8, single-key sequences, decode-only batches under the
+row blocks, every G in 1 .. 8 (G = 3, 5, 6, 7 give decode tiles whose
+rows do not divide 16), single-key sequences, decode-only batches under the
 split and page-balanced planners, and RoPE applied on load.
 """
 import random
@@ -22,13 +23,13 @@ from tests.gpu_helpers import assert_close_bf16, make_batch, oracle_paged
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 F8 = torch.float8_e4m3fn
-N_CASES = 64
+N_CASES = 96
 
 
 def _case(k):
     r = random.Random(1000 + k)
     Hkv = r.choice([1, 2, 4, 8])
-    G = r.choice([1, 2, 4, 8])
+    G = r.choice([1, 2, 3, 4, 5, 6, 7, 8])   # 3, 5, 6, 7: R = q_len * G does not divide 16
     D = r.choice([64, 128])
     bs = r.choice([8, 16, 32])
     kv8 = r.random() < 0.3

@@ -346,3 +346,104 @@ def test_oracle_qkv_identity_projection_is_rope_write():
     oa.kv_write(kc2, vc2, slots, k_rot, x.view(n, Hkv, D))
     assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
     assert torch.equal(q, k_rot)
+
+
+# ---------------------------------------------------------------- per-op rounding of apply_rope
+def _bf16_rne(x: np.ndarray) -> np.ndarray:
+    """fp32 -> nearest bf16 (ties to even), returned as fp32, from the bit
+    pattern (NaN kept quiet)."""
+    u = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    r = np.where(nan, (u | 0x400000) & 0xFFFF0000, r)
+    return r.astype(np.uint32).view(np.float32)
+
+
+def test_apply_rope_bf16_rounds_after_every_op():
+    """attention.py:105-118 in bf16 is six torch ops, each rounded to bf16:
+    lo = r(r(x1 c) - r(x2 s)), hi = r(r(x1 s) + r(x2 c)).  A numpy brute force
+    of exactly that (products exact in fp32, differences rounded to fp32 then
+    to bf16) must equal the oracle bit for bit, and on the same inputs a
+    single rounding of the exact result must differ often enough that the
+    check tells the two apart."""
+    g = torch.Generator().manual_seed(17)
+    D = 128
+    x = (torch.randn(4, 64, 2, D, generator=g) * 3).to(torch.bfloat16)
+    cos_t, sin_t = orope.rope_cache(4096, D, 500000.0, torch.bfloat16)
+    pos = torch.randint(0, 4096, (4, 64), generator=g)
+    c, s = cos_t[pos], sin_t[pos]
+    out = orope.apply_rope(x, c, s).float().numpy()
+    xf = x.float().numpy()
+    x1, x2 = xf[..., :D // 2], xf[..., D // 2:]
+    cf = c.float().numpy()[:, :, None, :]
+    sf = s.float().numpy()[:, :, None, :]
+    lo = _bf16_rne(_bf16_rne(x1 * cf) - _bf16_rne(x2 * sf))
+    hi = _bf16_rne(_bf16_rne(x1 * sf) + _bf16_rne(x2 * cf))
+    want = np.concatenate([lo, hi], axis=-1)
+    assert np.array_equal(out.view(np.uint32), want.view(np.uint32))
+    x164, x264 = x1.astype(np.float64), x2.astype(np.float64)
+    once = np.concatenate([_bf16_rne((x164 * cf - x264 * sf).astype(np.float32)),
+                           _bf16_rne((x164 * sf + x264 * cf).astype(np.float32))], axis=-1)
+    assert (once != want).mean() > 0.05
+
+
+def test_apply_rope_fp32_has_no_fused_multiply_add():
+    """In fp32 each product and the difference are rounded separately (torch
+    runs them as separate ops): numpy float32 arithmetic reproduces it bit for
+    bit, and a fused multiply-add or an fp64 evaluation would not."""
+    g = torch.Generator().manual_seed(18)
+    D = 64
+    x = torch.randn(3, 40, 2, D, generator=g)
+    cos_t, sin_t = orope.rope_cache(1000, D, 500000.0, torch.float32)
+    pos = torch.randint(0, 1000, (3, 40), generator=g)
+    c, s = cos_t[pos], sin_t[pos]
+    out = orope.apply_rope(x, c, s).numpy()
+    xf = x.numpy()
+    x1, x2 = xf[..., :D // 2], xf[..., D // 2:]
+    cf, sf = c.numpy()[:, :, None, :], s.numpy()[:, :, None, :]
+    want = np.concatenate([x1 * cf - x2 * sf, x1 * sf + x2 * cf], axis=-1)
+    assert np.array_equal(out.view(np.uint32), want.view(np.uint32))
+    x164, x264 = x1.astype(np.float64), x2.astype(np.float64)
+    exact = np.concatenate([(x164 * cf - x264 * sf), (x164 * sf + x264 * cf)], axis=-1).astype(np.float32)
+    assert (exact != want).mean() > 0.01
+
+
+# ---------------------------------------------------------------- RMSNorm / SiLU MLP (config (a)'s layer)
+def test_rms_norm_properties():
+    """norm.py:15-22: unit root-mean-square with unit weights, invariance to
+    a positive scale (eps = 0), elementwise weight, one-hot closed form."""
+    from oracle import engine as oe
+    g = torch.Generator().manual_seed(19)
+    x = torch.randn(5, 256, generator=g, dtype=torch.float64)
+    ones = torch.ones(256, dtype=torch.float64)
+    y = oe.rms_norm(x, ones, 0.0)
+    assert torch.allclose((y * y).mean(-1), torch.ones(5, dtype=torch.float64), atol=1e-12)
+    assert torch.allclose(oe.rms_norm(7.5 * x, ones, 0.0), y, atol=1e-12)
+    w = torch.randn(256, generator=g, dtype=torch.float64)
+    assert torch.allclose(oe.rms_norm(x, w, 0.0), y * w, atol=1e-12)
+    e = torch.zeros(1, 256, dtype=torch.float64)
+    e[0, 9] = -3.0
+    oh = oe.rms_norm(e, ones, 0.0)
+    assert abs(float(oh[0, 9]) + 16.0) < 1e-12 and float(oh.abs().sum()) == 16.0   # sqrt(256) * sign
+    yeps = oe.rms_norm(e, ones, 1e-5)                                               # eps inside the root
+    assert abs(float(yeps[0, 9]) + 3.0 / math.sqrt(9.0 / 256 + 1e-5)) < 1e-12
+
+
+def test_silu_mlp_properties():
+    """mlp.py:44-47, down(silu(gate x) * up x): with gate = up = down = I it is
+    x * silu(x), checked at known values of silu; linear in down; zero when
+    up = 0."""
+    from oracle import engine as oe
+    eye = torch.eye(4, dtype=torch.float64)
+    lw = {"gate": eye, "up": eye, "down": eye}
+    x = torch.tensor([[0.0, 1.0, -1.0, 2.0]], dtype=torch.float64)
+    silu = [0.0, 0.7310585786300049, -0.2689414213699951, 1.7615941559557649]   # z / (1 + e^-z)
+    want = torch.tensor([[xi * si for xi, si in zip([0.0, 1.0, -1.0, 2.0], silu)]], dtype=torch.float64)
+    assert torch.allclose(oe.mlp(x, lw), want, atol=1e-14)
+    g = torch.Generator().manual_seed(20)
+    lw2 = {k: torch.randn(8, 8, generator=g, dtype=torch.float64) for k in ("gate", "up", "down")}
+    xr = torch.randn(3, 8, generator=g, dtype=torch.float64)
+    lw3 = dict(lw2, down=2.5 * lw2["down"])
+    assert torch.allclose(oe.mlp(xr, lw3), 2.5 * oe.mlp(xr, lw2), atol=1e-12)
+    assert torch.equal(oe.mlp(xr, dict(lw2, up=torch.zeros(8, 8, dtype=torch.float64))),
+                       torch.zeros(3, 8, dtype=torch.float64))
