@@ -42,6 +42,9 @@ SIGNATURES = {
     "gllm_qkv_rope_kv_write": (ctypes.c_int, [_p, _i64, _i64, _i32, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i32,
                                               _p, _p, _i64, _i64, _p, _p, _i64, _p, _p, _p, _i64, _i32, _i32, _i32,
                                               _i32, _i32, _p, _sz, _p]),
+    "gllm_qkv_rope_kv_write_noalloc": (ctypes.c_int, [_p, _i64, _i64, _i32, _p, _i64, _p, _i64, _p, _i64, _p, _i64,
+                                                      _i32, _p, _p, _i64, _i64, _p, _p, _i64, _p, _p, _p, _i64, _i32,
+                                                      _i32, _i32, _i32, _i32, _p]),
     "gllm_qkv_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32, _i32]),
     "gllm_attention_dense": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p,
                                             _i64, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p]),

@@ -6,6 +6,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -291,6 +292,74 @@ int gllm_qkv_rope_kv_write(const void* x, int64_t x_row_stride, int64_t num_toke
   a.workspace = (float*)workspace; a.workspace_bytes = workspace ? workspace_bytes : 0;
   a.cus = device_cus();
   return hip_check(launch_qkv_rope_write(a, (hipStream_t)stream), "qkv projection launch");
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- no-alloc QKV
+// Scratch of gllm_qkv_rope_kv_write_noalloc: the split-K partial sums live in
+// this file-scope device array (one copy per GPU, held until the process
+// ends).  Host code never passes the array's name to a kernel: it is only a
+// host-side stand-in.  Its device address comes from hipGetSymbolAddress, once
+// per device with that device current, and that address is what the kernels
+// get.  Every call on a GPU shares the GPU's array, so calls that overlap on
+// one GPU race; each call fully rewrites the partials it reads (the partial
+// kernel stores every element before the finish kernel sums them), so no
+// clearing is needed.
+namespace {
+constexpr size_t kQkvScratchBytes = size_t(24) << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) char g_qkv_scratch[kQkvScratchBytes];
+void* g_qkv_scratch_ptr[kMaxDevices] = {};
+std::mutex g_qkv_scratch_mu;
+
+int qkv_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_check(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(GLLM_ATTN_EUNSUPPORTED, "device %d >= %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_qkv_scratch_mu);
+  if (!g_qkv_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_qkv_scratch));
+    if (e != hipSuccess) return hip_check(e, "hipGetSymbolAddress(qkv scratch)");
+    g_qkv_scratch_ptr[dev] = p;
+  }
+  *out = g_qkv_scratch_ptr[dev];
+  return ok();
+}
+}  // namespace
+
+extern "C" {
+
+int gllm_qkv_rope_kv_write_noalloc(const void* x, int64_t x_row_stride, int64_t num_tokens, int32_t hidden,
+                                   const void* w_q, int64_t w_q_row_stride, const void* w_k, int64_t w_k_row_stride,
+                                   const void* w_v, int64_t w_v_row_stride, void* q_out, int64_t q_out_row_stride,
+                                   int32_t rotate_q, void* k_cache, void* v_cache, int64_t cache_slot_stride,
+                                   int64_t num_slots, const int64_t* slot_mapping, const int32_t* query_lens,
+                                   int64_t tokens_per_seq, const void* cos, const void* sin, const int64_t* rope_rows,
+                                   int64_t rope_row_stride, int32_t num_q_heads, int32_t num_kv_heads,
+                                   int32_t head_dim, int32_t dtype, int32_t kv_dtype, void* stream) {
+  if (num_tokens < 0 || hidden <= 0 || num_kv_heads <= 0 || num_q_heads <= 0)
+    return gllm_qkv_rope_kv_write(x, x_row_stride, num_tokens, hidden, w_q, w_q_row_stride, w_k, w_k_row_stride,
+                                  w_v, w_v_row_stride, q_out, q_out_row_stride, rotate_q, k_cache, v_cache,
+                                  cache_slot_stride, num_slots, slot_mapping, query_lens, tokens_per_seq, cos, sin,
+                                  rope_rows, rope_row_stride, num_q_heads, num_kv_heads, head_dim, dtype, kv_dtype,
+                                  nullptr, 0, stream);   // the argument checks and their messages
+  const size_t need = gllm_qkv_workspace_bytes(num_tokens, hidden, num_q_heads, num_kv_heads, head_dim, q_out != nullptr);
+  if (need > kQkvScratchBytes)
+    return fail(GLLM_ATTN_EUNSUPPORTED,
+                "this batch's split-K partials need %zu bytes, more than the %zu-byte static scratch of the "
+                "no-alloc entry point; call gllm_qkv_rope_kv_write with a workspace", need, kQkvScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    if (int rc = qkv_scratch(&ws)) return rc;
+  }
+  return gllm_qkv_rope_kv_write(x, x_row_stride, num_tokens, hidden, w_q, w_q_row_stride, w_k, w_k_row_stride,
+                                w_v, w_v_row_stride, q_out, q_out_row_stride, rotate_q, k_cache, v_cache,
+                                cache_slot_stride, num_slots, slot_mapping, query_lens, tokens_per_seq, cos, sin,
+                                rope_rows, rope_row_stride, num_q_heads, num_kv_heads, head_dim, dtype, kv_dtype,
+                                ws, need, stream);
 }
 
 size_t gllm_qkv_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t num_q_heads, int32_t num_kv_heads,

@@ -126,6 +126,28 @@ size_t gllm_qkv_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t num_
                                 int32_t head_dim, int32_t with_q);
 
 /*
+ * gllm_qkv_rope_kv_write without a workspace argument and without any
+ * allocation (no hipMalloc/hipFree, no allocating library call).  No
+ * counterpart in the reference: it is for callers that cannot allocate (code
+ * under HIP graph capture, serving loops and harnesses that forbid it).  The
+ * split-K partial sums of few-token batches go to a static 24 MiB device
+ * array inside the library, one per GPU, held until the process ends; a
+ * batch whose partials would need more (gllm_qkv_workspace_bytes > 24 MiB; every Llama-3 decode shape fits)
+ * is rejected with GLLM_ATTN_EUNSUPPORTED.  Every call on one GPU shares that
+ * GPU's array: calls that overlap on the same GPU (different streams, or
+ * threads) race.  Results equal gllm_qkv_rope_kv_write's with a workspace of
+ * gllm_qkv_workspace_bytes bytes.
+ */
+int gllm_qkv_rope_kv_write_noalloc(const void* x, int64_t x_row_stride, int64_t num_tokens, int32_t hidden,
+                                   const void* w_q, int64_t w_q_row_stride, const void* w_k, int64_t w_k_row_stride,
+                                   const void* w_v, int64_t w_v_row_stride, void* q_out, int64_t q_out_row_stride,
+                                   int32_t rotate_q, void* k_cache, void* v_cache, int64_t cache_slot_stride,
+                                   int64_t num_slots, const int64_t* slot_mapping, const int32_t* query_lens,
+                                   int64_t tokens_per_seq, const void* cos, const void* sin, const int64_t* rope_rows,
+                                   int64_t rope_row_stride, int32_t num_q_heads, int32_t num_kv_heads,
+                                   int32_t head_dim, int32_t dtype, int32_t kv_dtype, void* stream);
+
+/*
  * Rotate k (and, if q_out != NULL, q) with rotate-half RoPE and write k/v rows
  * into the paged cache.  Token t (0 <= t < num_tokens) writes slot
  * slot_mapping[t] of k_cache / v_cache (each [num_slots, cache_slot_stride]).
