@@ -1,6 +1,6 @@
 """Benchmark of the gLLM attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs d,c,b,e]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs d,c,b,a,e]
 
 Prints ONE JSON line.  The headline (``value``) is BASELINE config (d), the
 metric's 8B GQA shape: one paged-attention launch over a mixed continuous
@@ -249,6 +249,82 @@ def bench_metadata(b: workloads.PagedBatch, warmup, reps, dev, cpu: bool):
     return res
 
 
+def bench_decode_step(dtype, warmup, reps, dev):
+    """One decode step of a config (a)-shaped model's attention path (16
+    layers of Llama-3.2-1B heads, 8 sequences, block size 16): per layer the
+    RoPE + KV write and the paged attention (``Attention.attention``), 32
+    launches.  Eager launches from Python vs the same step captured in one
+    HIP graph; returns both per-step times (median over ``reps``)."""
+    import gllm_amd
+    L, Hq, Hkv, D, bs, B = 16, 32, 8, 64, 16, 8
+    g = torch.Generator().manual_seed(31)
+    ctx = torch.randint(20, 200, (B,), generator=g).tolist()
+    seq = [c + 1 for c in ctx]
+    cache = gllm_amd.PagedKVCache(L, Hkv, D, bs, B, 256, dtype, dev)
+    cache.physical_kv_cache.normal_()
+    bt = workloads.block_tables(seq, bs, cache.num_blocks).to(dev)
+    rows = torch.arange(B)
+    pos = torch.tensor(ctx)
+    qsm = (bt.cpu()[rows, pos // bs].to(torch.int64) * bs + pos % bs).view(B, 1).to(dev)
+    gm = gllm_amd.AttentionMetadata(query_lens=torch.ones(B, dtype=torch.int32, device=dev),
+                                    seq_lens=torch.tensor(seq, dtype=torch.int32, device=dev), max_seq_len=max(seq),
+                                    block_table=bt, slot_mapping=None, query_slot_mapping=qsm, bias=None,
+                                    block_size=bs)
+    ang = pos.unsqueeze(1) * 500000.0 ** (-2 * torch.arange(D // 2) / D)
+    cos, sin = torch.cos(ang).to(dtype).view(B, 1, -1).to(dev), torch.sin(ang).to(dtype).view(B, 1, -1).to(dev)
+
+    class Cfg:
+        num_attn_heads, num_kv_heads, head_dim, hidden_size = Hq, Hkv, D, Hq * D
+
+    Cfg.dtype = dtype
+    atts = [gllm_amd.Attention(li, Cfg, {f"model.layers.{li}.self_attn.{n}_proj.weight": torch.zeros(1)
+                                         for n in "qkvo"}) for li in range(L)]
+    qs = [torch.randn(B, 1, Hq, D, device=dev).to(dtype) for _ in range(L)]
+    ks = [torch.randn(B, 1, Hkv, D, device=dev).to(dtype) for _ in range(L)]
+    vs = [torch.randn(B, 1, Hkv, D, device=dev).to(dtype) for _ in range(L)]
+
+    def step():
+        for li in range(L):
+            atts[li].attention(qs[li], ks[li], vs[li], cos, sin, cache.get_layer_kv_cache(li), gm)
+
+    step()                                         # builds the plan once
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for s_, e_ in ev:
+        s_.record()
+        step()
+        e_.record()
+    torch.cuda.synchronize()
+    eager = statistics.median(s_.elapsed_time(e_) for s_, e_ in ev)
+    per, _ = graph_reps([step], warmup, reps, 1)
+    graph = statistics.median(per)
+    return {"layers": L, "seqs": B, "dtype": str(dtype).replace("torch.", ""), "launches_per_step": 2 * L,
+            "eager_ms_per_step": eager, "graph_ms_per_step": graph, "saving_ms": eager - graph,
+            "speedup": eager / graph}
+
+
+def bench_plan_host(b: workloads.PagedBatch, reps: int, dev):
+    """Host cost of one engine step's plan (what plan_for pays once per step):
+    create (planner + pinned staging from the library's pool), device
+    workspace (torch's caching allocator), upload (an enqueued copy), destroy
+    (staging back to the pool).  Median over ``reps`` after a warm-up."""
+    def once():
+        t = time.perf_counter()
+        p = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=b.num_q_heads, num_kv_heads=b.num_kv_heads,
+                                head_dim=b.head_dim, block_size=b.block_size, dtype=b.dtype, device=dev)
+        del p
+        return (time.perf_counter() - t) * 1e3
+    for _ in range(3):
+        once()
+    torch.cuda.synchronize()
+    ts = [once() for _ in range(reps)]
+    torch.cuda.synchronize()
+    return {"seqs": len(b.q_lens), "host_ms_median": statistics.median(ts), "host_ms_max": max(ts)}
+
+
 # ------------------------------------------------------------------ CPU baseline
 def _cpu_setup():
     cores = len(os.sched_getaffinity(0))
@@ -348,7 +424,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=60, help="timed steps (graph replays) of the headline config")
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="d,c,b,e")
+    ap.add_argument("--configs", default="d,c,b,a,e")
     ap.add_argument("--split", type=int, default=0, help="decode split tokens (0 = planner's choice)")
     ap.add_argument("--hw", type=int, default=0, help="kv heads per decode workgroup (0 = planner's choice)")
     ap.add_argument("--copies", type=int, default=4, help="KV pool copies rotated for config (b)")
@@ -419,6 +495,13 @@ def main():
         torch.cuda.empty_cache()
         # fused QKV projection + RoPE + KV write for the same 64 decode tokens (1B layer)
         extra["qkv_decode_1b"] = bench_qkv(64, 2048, 32, 8, 64, 24, args.warmup, max(10, reps // 3), dev)
+        torch.cuda.empty_cache()
+    if "a" in cfgs:
+        # config (a)'s decode step: 16 layers x (RoPE + KV write, paged attention), eager vs one HIP graph
+        extra["decode_step_1b_fp32"] = bench_decode_step(torch.float32, args.warmup, max(10, reps // 2), dev)
+        extra["decode_step_1b_bf16"] = bench_decode_step(torch.bfloat16, args.warmup, max(10, reps // 2), dev)
+        extra["plan_host_mixed_8b"] = bench_plan_host(workloads.config_d(), 50, dev)
+        extra["plan_host_decode_1b"] = bench_plan_host(workloads.config_b(), 50, dev)
         torch.cuda.empty_cache()
     if "e" in cfgs:
         e = workloads.config_e()

@@ -59,6 +59,74 @@ int device_cus() {
   return 256;
 }
 
+// Pinned staging buffers of plans, reused across plans (an engine builds one
+// plan per step): plan_create takes the smallest free buffer that fits and
+// plan_destroy hands it back, together with the event of its upload copy; a
+// buffer whose copy has not finished yet is only reused once that event has
+// completed (checked without blocking).  No hipHostMalloc / hipHostFree on the
+// steady-state path; the pool keeps at most kPoolKeep bytes.
+struct PinnedPool {
+  struct Buf { void* p; size_t n; hipEvent_t done; };
+  std::mutex mu;
+  std::vector<Buf> free_bufs;   // done == nullptr or completed
+  size_t kept = 0;
+  static constexpr size_t kPoolKeep = size_t(64) << 20;
+
+  static bool ready(const Buf& b) {
+    if (!b.done) return true;
+    const hipError_t e = hipEventQuery(b.done);
+    if (e == hipErrorNotReady) return false;
+    (void)hipGetLastError();
+    return true;
+  }
+  // A pinned buffer of at least n bytes (rounded up to a power of two >= 64 KB).
+  void* acquire(size_t n, size_t* cap) {
+    {
+      std::lock_guard<std::mutex> lk(mu);
+      size_t best = free_bufs.size();
+      for (size_t i = 0; i < free_bufs.size(); ++i)
+        if (free_bufs[i].n >= n && (best == free_bufs.size() || free_bufs[i].n < free_bufs[best].n) &&
+            ready(free_bufs[i]))
+          best = i;
+      if (best < free_bufs.size()) {
+        Buf b = free_bufs[best];
+        free_bufs.erase(free_bufs.begin() + best);
+        kept -= b.n;
+        if (b.done) (void)hipEventDestroy(b.done);
+        *cap = b.n;
+        return b.p;
+      }
+    }
+    size_t c = size_t(64) << 10;
+    while (c < n) c <<= 1;
+    void* p = nullptr;
+    if (hipHostMalloc(&p, c, hipHostMallocDefault) != hipSuccess) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    *cap = c;
+    return p;
+  }
+  // Takes ownership of `done` (may be null).
+  void release(void* p, size_t n, hipEvent_t done) {
+    std::lock_guard<std::mutex> lk(mu);
+    if (kept + n > kPoolKeep) {
+      if (done) {
+        (void)hipEventSynchronize(done);   // the copy must finish before the free
+        (void)hipEventDestroy(done);
+      }
+      (void)hipHostFree(p);
+      return;
+    }
+    free_bufs.push_back(Buf{p, n, done});
+    kept += n;
+  }
+};
+PinnedPool& pinned_pool() {
+  static PinnedPool* pool = new PinnedPool();   // never destroyed: buffers live until the process ends
+  return *pool;
+}
+
 }  // namespace
 
 struct gllm_attn_plan {
@@ -72,8 +140,9 @@ struct gllm_attn_plan {
   // page-balanced decode: workgroup w runs segs[seg_ptr[w] .. seg_ptr[w + 1])
   std::vector<DecodeSeg> segs;
   std::vector<int32_t> seg_ptr;
-  // staging copy of [items | seqs] in pinned host memory, device offsets
+  // staging copy of [items | seqs] in pinned host memory (from the pool), device offsets
   void* pinned = nullptr;
+  size_t pinned_cap = 0;
   bool pinned_is_host_malloc = false;  // hipHostMalloc unavailable (no device): plain malloc
   size_t off_items = 0, off_seqs = 0, off_segs = 0, off_segptr = 0, off_ctr = 0, off_ml = 0, off_part = 0, ws_bytes = 0;
   char* ws = nullptr;
@@ -587,8 +656,8 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
   p->ws_bytes = std::max<size_t>(o, 256);
   const size_t stage = p->off_ctr;
   if (stage > 0) {
-    if (hipHostMalloc(&p->pinned, stage, hipHostMallocDefault) != hipSuccess) {
-      (void)hipGetLastError();
+    p->pinned = pinned_pool().acquire(stage, &p->pinned_cap);
+    if (!p->pinned) {
       p->pinned = std::malloc(stage);
       p->pinned_is_host_malloc = true;
       if (!p->pinned) {
@@ -641,15 +710,15 @@ int gllm_attn_plan_upload(gllm_attn_plan* p, void* workspace, size_t bytes, void
 
 int gllm_attn_plan_destroy(gllm_attn_plan* p) {
   if (!p) return ok();
-  if (p->upload_done) {
-    (void)hipEventSynchronize(p->upload_done);  // the staging copy must finish before the free
-    (void)hipEventDestroy(p->upload_done);
-  }
-  if (p->pinned) {
-    if (p->pinned_is_host_malloc)
-      std::free(p->pinned);
-    else
-      (void)hipHostFree(p->pinned);
+  if (p->pinned && !p->pinned_is_host_malloc) {
+    // back to the pool with the upload's event: reused once the copy is done
+    pinned_pool().release(p->pinned, p->pinned_cap, p->upload_done);
+  } else {
+    if (p->upload_done) {
+      (void)hipEventSynchronize(p->upload_done);  // the staging copy must finish before the free
+      (void)hipEventDestroy(p->upload_done);
+    }
+    if (p->pinned) std::free(p->pinned);
   }
   delete p;
   return ok();

@@ -1,6 +1,6 @@
 // fp32 attention (model dtype float32): paged decode/prefill and the dense-bias
-// op.  One wave per (query head, query row, sequence); lanes split the head
-// dim, keys are visited in order with an exact online softmax (expf).  This is
+// op.  One wave per (query head, query row, sequence), 64 keys per step, exact
+// online softmax (expf).  This is
 // the path for fp32 models (BASELINE config (a)); the bf16 MFMA kernels are the
 // performance path.  Compiled with -ffp-contract=off so the q rotation rounds
 // each op like the reference (gllm/model/layers/attention.py:105-118).
@@ -15,8 +15,15 @@ template <> __device__ __forceinline__ float ldkv<__bf16>(const __bf16* p) { ret
 // fp8 e4m3fn cache: exact widening (the reference's .to(model dtype) after the gather)
 template <> __device__ __forceinline__ float ldkv<fp8e4m3>(const fp8e4m3* p) { return __builtin_amdgcn_cvt_f32_fp8((int)p->bits, 0); }
 
+// One wave per (query head, query row, sequence).  Keys go 64 at a time: lane
+// j scores key p0 + j against q (q read from LDS, so every lane has all of
+// it), one wave max / sum per chunk updates the exact online softmax (expf),
+// then the lanes switch to the head dims (d = lane + 64 i) and accumulate the
+// chunk's p-weighted V rows, each key's p and slot read out of its lane.  Two
+// memory round trips per 64 keys instead of one per key.
 template <bool DENSE, typename KV>
 __global__ void __launch_bounds__(64) attn_f32_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float qs[256];
   const int hq = blockIdx.x, r = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
   const int D = a.head_dim;
   int ctx, qlen, L;
@@ -40,61 +47,104 @@ __global__ void __launch_bounds__(64) attn_f32_kernel(AttnArgs a) {
   const int half = D / 2;
   const float* qp = (const float*)a.q + qrow * a.q_row_stride + (int64_t)hq * D;
 
-  float q[4], acc[4];
+  float acc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int d = lane + 64 * i;
     acc[i] = 0.f;
-    q[i] = 0.f;
     if (d < D) {
-      q[i] = qp[d];
+      float qv = qp[d];
       if (!DENSE && a.rope_mode != kRopeNone) {
         const int64_t crow = a.rope_mode == kRopeByPosition ? (int64_t)(ctx + r) : qrow;
         const float* cp = (const float*)a.rope_cos + crow * a.rope_row_stride;
         const float* sp = (const float*)a.rope_sin + crow * a.rope_row_stride;
         if (d < half) {
-          q[i] = __fsub_rn(__fmul_rn(qp[d], cp[d]), __fmul_rn(qp[d + half], sp[d]));
+          qv = __fsub_rn(__fmul_rn(qp[d], cp[d]), __fmul_rn(qp[d + half], sp[d]));
         } else {
           const int j = d - half;
-          q[i] = __fadd_rn(__fmul_rn(qp[j], sp[j]), __fmul_rn(qp[d], cp[j]));
+          qv = __fadd_rn(__fmul_rn(qp[j], sp[j]), __fmul_rn(qp[d], cp[j]));
         }
       }
+      qs[d] = qv;
     }
   }
+  __syncthreads();
   const int nkeys = DENSE ? L : ctx + r + 1;
   const int32_t* bt = DENSE ? nullptr : a.block_table + (int64_t)b * a.block_table_stride;
+  const KV* kbase = DENSE ? (const KV*)a.k + (int64_t)b * a.k_batch_stride + (int64_t)kvh * D
+                          : (const KV*)a.k_cache + (int64_t)kvh * D;
+  const KV* vbase = DENSE ? (const KV*)a.v + (int64_t)b * a.v_batch_stride + (int64_t)kvh * D
+                          : (const KV*)a.v_cache + (int64_t)kvh * D;
+  const int64_t kstride = DENSE ? a.k_row_stride : a.cache_slot_stride;
+  const int64_t vstride = DENSE ? a.v_row_stride : a.cache_slot_stride;
+  const float* brow = DENSE ? (const float*)a.bias + (int64_t)b * a.bias_batch_stride + (int64_t)r * a.bias_row_stride
+                            : nullptr;
   float m = kNegInf, l = 0.f;
-  for (int p = 0; p < nkeys; ++p) {
-    const KV *kp, *vp;
-    if (DENSE) {
-      kp = (const KV*)a.k + (int64_t)b * a.k_batch_stride + (int64_t)p * a.k_row_stride + (int64_t)kvh * D;
-      vp = (const KV*)a.v + (int64_t)b * a.v_batch_stride + (int64_t)p * a.v_row_stride + (int64_t)kvh * D;
-    } else {
-      uint32_t blk = (uint32_t)bt[p >> a.block_shift];
-      if (blk >= (uint64_t)a.num_blocks) blk = 0;
-      const int64_t slot = (int64_t)blk * a.block_size + (p & (a.block_size - 1));
-      kp = (const KV*)a.k_cache + slot * a.cache_slot_stride + (int64_t)kvh * D;
-      vp = (const KV*)a.v_cache + slot * a.cache_slot_stride + (int64_t)kvh * D;
+  for (int p0 = 0; p0 < nkeys; p0 += 64) {
+    const int p = p0 + lane;
+    const bool valid = p < nkeys;
+    // row of key p in k (dense) or in the paged cache
+    int64_t row = 0;
+    if (valid) {
+      if (DENSE) {
+        row = p;
+      } else {
+        uint32_t blk = (uint32_t)bt[p >> a.block_shift];
+        if (blk >= (uint64_t)a.num_blocks) blk = 0;   // never address outside the pool
+        row = (int64_t)blk * a.block_size + (p & (a.block_size - 1));
+      }
     }
-    float part = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = lane + 64 * i;
-      if (d < D) part += q[i] * ldkv<KV>(kp + d);
+    float s = kNegInf;
+    if (valid) {
+      const KV* kp = kbase + row * kstride;
+      float dot = 0.f;
+      int d = 0;
+      for (; d + 4 <= D; d += 4) {
+        const f32x4 qv = *reinterpret_cast<const f32x4*>(qs + d);
+        dot += qv[0] * ldkv<KV>(kp + d) + qv[1] * ldkv<KV>(kp + d + 1) + qv[2] * ldkv<KV>(kp + d + 2) +
+               qv[3] * ldkv<KV>(kp + d + 3);
+      }
+      for (; d < D; ++d) dot += qs[d] * ldkv<KV>(kp + d);   // head dims not a multiple of 4
+      s = dot * a.scale;
+      if (DENSE) s += brow[p];
     }
+    float cm = s;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off);
-    float s = part * a.scale;
-    if (DENSE) s += ((const float*)a.bias)[(int64_t)b * a.bias_batch_stride + (int64_t)r * a.bias_row_stride + p];
-    if (s == kNegInf) continue;
-    const float mn = fmaxf(m, s);
-    const float alpha = expf(m - mn);
-    const float e = expf(s - mn);
-    l = l * alpha + e;
+    for (int off = 32; off >= 1; off >>= 1) cm = fmaxf(cm, __shfl_xor(cm, off));
+    if (cm == kNegInf) continue;                       // every key of the chunk masked
+    const float mn = fmaxf(m, cm);
+    const float alpha = expf(m - mn);                  // m = -inf: 0
+    const float e = s == kNegInf ? 0.f : expf(s - mn);
+    float es = e;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = lane + 64 * i;
-      if (d < D) acc[i] = acc[i] * alpha + e * ldkv<KV>(vp + d);
+    for (int off = 32; off >= 1; off >>= 1) es += __shfl_xor(es, off);
+    l = l * alpha + es;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] *= alpha;
+    const int nk = min(64, nkeys - p0);
+    const int rlo = (int)(uint32_t)row, rhi = (int)((uint64_t)row >> 32);
+    // 8 keys' V rows in flight at a time (keys past the chunk re-read its last
+    // row with weight 0), summed in key order
+    for (int j0 = 0; j0 < nk; j0 += 8) {
+      float pj[8], vv[8][4];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = min(j0 + u, nk - 1);
+        const float pe = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(e), j));
+        pj[u] = j0 + u < nk ? pe : 0.f;
+        const int64_t rj = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane(rhi, j) << 32) |
+                                     (uint32_t)__builtin_amdgcn_readlane(rlo, j));
+        const KV* vp = vbase + rj * vstride;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = lane + 64 * i;
+          vv[u][i] = d < D ? ldkv<KV>(vp + d) : 0.f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] += pj[u] * vv[u][i];
     }
     m = mn;
   }

@@ -52,3 +52,69 @@ def test_graph_replay_matches_eager(name):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out[: b.rows].view(torch.int16), eager[: b.rows].view(torch.int16)), f"{name} replay {rep}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_whole_decode_step_graph(dtype):
+    """One decode step of a config (a)-shaped model (16 layers, Llama-3.2-1B
+    heads, block size 16, 8 sequences) as the layer loop of model.py:202-222
+    runs it: per layer the RoPE + KV write and the paged attention
+    (Attention.attention, attention.py:151-178), all 32 launches captured in
+    one HIP graph.  Every replay (with eager work between) equals the eager
+    step bit for bit in every layer's output and in the written cache."""
+    import gllm_amd
+    from oracle import metadata as om
+    from oracle import rope as orope
+    print(f"whole decode step graph {dtype}", flush=True)
+    L, Hq, Hkv, D, bs, B = 16, 32, 8, 64, 16, 8
+    g = torch.Generator().manual_seed(31)
+    ctx = torch.randint(20, 200, (B,), generator=g).tolist()
+    ql = [1] * B
+    cache = gllm_amd.PagedKVCache(L, Hkv, D, bs, B, 256, dtype, "cuda")
+    cache.physical_kv_cache.copy_(torch.randn(cache.physical_kv_cache.shape, generator=g).to(dtype))
+    bt = om.random_block_tables([c + 1 for c in ctx], bs, cache.num_blocks, g, width=16)
+    meta = om.build_metadata(ctx, ql, bt, bs, dtype)
+    gm = gllm_amd.AttentionMetadata(
+        query_lens=meta.query_lens.cuda(), seq_lens=meta.seq_lens.cuda(), max_seq_len=meta.max_seq_len,
+        block_table=meta.block_table.cuda(), slot_mapping=meta.slot_mapping.cuda(),
+        query_slot_mapping=meta.query_slot_mapping.cuda(), bias=None, block_size=bs)
+    cos_t, sin_t = orope.rope_cache(256, D, 500000.0, dtype)
+    pos = meta.positions
+    cos, sin = cos_t[pos].cuda(), sin_t[pos].cuda()
+
+    class Cfg:
+        num_attn_heads, num_kv_heads, head_dim, hidden_size = Hq, Hkv, D, Hq * D
+
+    Cfg.dtype = dtype
+    w = lambda li: {f"model.layers.{li}.self_attn.{n}_proj.weight": torch.zeros(1) for n in "qkvo"}
+    atts = [gllm_amd.Attention(li, Cfg, w(li)) for li in range(L)]
+    qs = [torch.randn(B, 1, Hq, D, generator=g).to(dtype).cuda() for _ in range(L)]
+    ks = [torch.randn(B, 1, Hkv, D, generator=g).to(dtype).cuda() for _ in range(L)]
+    vs = [torch.randn(B, 1, Hkv, D, generator=g).to(dtype).cuda() for _ in range(L)]
+
+    def step():
+        return [atts[li].attention(qs[li], ks[li], vs[li], cos, sin, cache.get_layer_kv_cache(li), gm)
+                for li in range(L)]
+
+    eager = [o.clone() for o in step()]                  # also builds the plan, once for all layers
+    cache_after = cache.physical_kv_cache.clone()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step()
+    bits = (lambda t: t.view(torch.int32)) if dtype == torch.float32 else (lambda t: t.view(torch.int16))
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))                        # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for li in range(L):
+            assert torch.equal(bits(outs[li]), bits(eager[li])), f"replay {rep} layer {li}"
+        assert torch.equal(cache.physical_kv_cache.view(torch.uint8), cache_after.view(torch.uint8))

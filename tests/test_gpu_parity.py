@@ -256,6 +256,24 @@ def test_fp32_paged_parity():
     assert d < 1e-4, d
 
 
+@pytest.mark.parametrize("D,kv", [(64, torch.float32), (128, torch.float32), (50, torch.float32),
+                                  (256, torch.float32), (64, torch.bfloat16), (128, torch.float8_e4m3fn)])
+def test_fp32_paged_long_contexts(D, kv):
+    """fp32 model: keys go 64 per step, so contexts of several steps (with
+    ragged last steps and block-boundary lengths), head dims that are not a
+    multiple of 4, and bf16 / fp8 caches (widened on load)."""
+    print(f"fp32 paged long D={D} kv={kv}", flush=True)
+    b = make_batch([0, 63, 64, 65, 300, 1000], [70, 1, 1, 1, 9, 1], 8, 2, D, dtype=torch.float32)
+    if kv != torch.float32:
+        b.k_cache, b.v_cache = b.k_cache.to(kv), b.v_cache.to(kv)
+    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=8, num_kv_heads=2, head_dim=D,
+                               block_size=16, dtype=torch.float32, device=DEV)
+    out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
+    torch.cuda.synchronize()
+    d = (out.cpu() - oracle_paged(b)).abs().max().item()
+    assert d < 1e-4, d
+
+
 # ------------------------------------------------------------ dense-bias op
 @pytest.mark.parametrize("B,Tq,T,Hq,Hkv,D", [(1, 8, 8, 1, 1, 128), (1, 16, 16, 1, 1, 128), (1, 40, 40, 1, 1, 128),
                                              (1, 256, 256, 1, 1, 128), (1, 32, 256, 1, 1, 128),
