@@ -49,6 +49,15 @@ int log2i(int64_t x) {
 }
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// Constants of the device division by the block size (div_bs in common.h):
+// k = ceil(log2 bs), magic = ceil(2^(31+k) / bs) (< 2^32 for every bs >= 1).
+void block_div(int32_t bs, uint32_t* magic, int32_t* shift) {
+  const int k = log2i(bs);
+  *magic = (uint32_t)(((uint64_t(1) << (31 + k)) + (uint64_t)bs - 1) / (uint64_t)bs);
+  *shift = k;
+}
+constexpr int32_t kMaxBlockSize = 65536;
+
 // Compute units of the current device (256 when there is none, e.g. a CPU-only host).
 int device_cus() {
   int dev = 0;
@@ -199,7 +208,9 @@ void plan_balanced_decode(gllm_attn_plan* p, int cus, int heads_req) {
   const BalancedShape shape = balanced_shape(p, cus, heads_req);
   const int hw = shape.hw, hgroups = shape.hgroups;
   const int64_t bs = p->bs;
-  const int64_t ucap = std::max<int64_t>(1, (bs <= 16 ? 512 * bs : 510 * bs) / 16);
+  // a segment's keys start on a 16-key unit, so a block size that is not a
+  // power of two <= 16 can add one partial block at the front: stay <= 511
+  const int64_t ucap = std::max<int64_t>(1, (is_pow2(bs) && bs <= 16 ? 512 * bs : 510 * bs) / 16);
   const int64_t U = shape.units, W = shape.wgs;
   p->heads_per_wg = hw;
   p->decode_waves = 8;
@@ -258,8 +269,8 @@ int gllm_build_metadata(const int32_t* block_table, int64_t block_table_stride, 
   if (num_seqs == 0) return ok();
   if (!block_table || !seq_lens || !query_lens) return fail(GLLM_ATTN_EINVAL, "null block_table or lengths");
   if (!slot_mapping && !positions && !cu_seqlens) return fail(GLLM_ATTN_EINVAL, "nothing to do: no output given");
-  if (block_size <= 0 || (block_size & (block_size - 1)))
-    return fail(GLLM_ATTN_EUNSUPPORTED, "block_size %d must be a power of two", block_size);
+  if (block_size <= 0 || block_size > kMaxBlockSize)
+    return fail(GLLM_ATTN_EINVAL, "block_size %d must be in [1, %d]", block_size, kMaxBlockSize);
   if (block_table_width <= 0 || block_table_stride < block_table_width)
     return fail(GLLM_ATTN_EINVAL, "block_table width %lld / stride %lld invalid", (long long)block_table_width,
                 (long long)block_table_stride);
@@ -270,7 +281,8 @@ int gllm_build_metadata(const int32_t* block_table, int64_t block_table_stride, 
   MetadataArgs a{};
   a.block_table = block_table; a.block_table_stride = block_table_stride; a.bt_width = block_table_width;
   a.seq_lens = seq_lens; a.query_lens = query_lens; a.num_seqs = num_seqs; a.q_seq_stride = q_seq_stride;
-  a.block_size = block_size; a.block_shift = __builtin_ctz((unsigned)block_size);
+  a.block_size = block_size;
+  block_div(block_size, &a.block_magic, &a.block_shift);
   a.slot_mapping = slot_mapping; a.positions = positions; a.cu_seqlens = cu_seqlens; a.num_rows = num_rows;
   return hip_check(launch_build_metadata(a, (hipStream_t)stream), "build_metadata launch");
 }
@@ -449,7 +461,8 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
   if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0)
     return fail(GLLM_ATTN_EINVAL, "num_q_heads (%d) must be a positive multiple of num_kv_heads (%d)",
                 num_q_heads, num_kv_heads);
-  if (!is_pow2(block_size)) return fail(GLLM_ATTN_EUNSUPPORTED, "block_size %d is not a power of two", block_size);
+  if (block_size <= 0 || block_size > kMaxBlockSize)
+    return fail(GLLM_ATTN_EINVAL, "block_size %d must be in [1, %d]", block_size, kMaxBlockSize);
   if (dtype == GLLM_DTYPE_BF16) {
     if (head_dim != 64 && head_dim != 128)
       return fail(GLLM_ATTN_EUNSUPPORTED, "bf16 kernels support head_dim 64 and 128, not %d", head_dim);
@@ -762,7 +775,8 @@ int gllm_paged_attention(const gllm_attn_plan* p, const void* q, int64_t q_row_s
   a.q = q; a.q_row_stride = q_row_stride; a.out = out; a.out_row_stride = out_row_stride;
   a.k_cache = k_cache; a.v_cache = v_cache; a.cache_slot_stride = cache_slot_stride; a.num_blocks = num_blocks;
   a.block_table = block_table; a.block_table_stride = block_table_stride;
-  a.block_size = p->bs; a.block_shift = log2i(p->bs);
+  a.block_size = p->bs;
+  block_div(p->bs, &a.block_magic, &a.block_shift);
   a.rope_cos = rope_cos; a.rope_sin = rope_sin; a.rope_row_stride = rope_row_stride; a.rope_mode = rope_mode;
   a.seqs = (const SeqInfo*)(p->ws + p->off_seqs);
   a.items = (const WorkItem*)(p->ws + p->off_items);

@@ -89,9 +89,10 @@ __global__ void __launch_bounds__(64) attn_f32_kernel(AttnArgs a) {
       if (DENSE) {
         row = p;
       } else {
-        uint32_t blk = (uint32_t)bt[p >> a.block_shift];
+        const uint32_t bi = div_bs((uint32_t)p, a.block_magic, a.block_shift);
+        uint32_t blk = (uint32_t)bt[bi];
         if (blk >= (uint64_t)a.num_blocks) blk = 0;   // never address outside the pool
-        row = (int64_t)blk * a.block_size + (p & (a.block_size - 1));
+        row = (int64_t)blk * a.block_size + (p - (int)bi * a.block_size);
       }
     }
     float s = kNegInf;

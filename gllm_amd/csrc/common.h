@@ -188,6 +188,16 @@ __device__ __forceinline__ float sum_xor32(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Division by the KV block size (any size >= 1): floor(p / bs) for
+// 0 <= p < 2^31 is umulhi(2p, magic) >> shift with k = ceil(log2 bs),
+// magic = ceil(2^(31+k) / bs), shift = k.  Exact: with e = magic bs - 2^(31+k)
+// (0 <= e < bs <= 2^k) the quotient is p / bs + p e / (bs 2^(31+k)), and
+// p e < 2^(31+k) keeps the error term below 1/bs.  A power of two 2^k gives
+// magic = 2^31, i.e. p >> k.
+__device__ __forceinline__ uint32_t div_bs(uint32_t p, uint32_t magic, int shift) {
+  return __umulhi(p << 1, magic) >> shift;
+}
+
 // Sequence / work descriptors shared by host planner and kernels.
 struct SeqInfo {
   int32_t q_row_start;   // first query row of the sequence in q / out

@@ -45,8 +45,9 @@ struct AttnArgs {
   int64_t num_blocks;
   const int32_t* block_table;
   int64_t block_table_stride;
-  int32_t block_size;
-  int32_t block_shift;        // log2(block_size) (block_size is a power of two)
+  int32_t block_size;         // any size >= 1
+  uint32_t block_magic;       // floor(p / block_size) = div_bs(p, block_magic, block_shift)
+  int32_t block_shift;
   // dense source (reference_attention contract); q/out rows are b * q_seq_stride + r
   const void* k;
   const void* v;
@@ -90,7 +91,8 @@ struct MetadataArgs {
   const int32_t* query_lens;
   int32_t num_seqs;
   int64_t q_seq_stride;         // > 0: padded [B, q_seq_stride] rows; 0: packed
-  int32_t block_size, block_shift;
+  int32_t block_size, block_shift;   // div_bs(p, block_magic, block_shift) = p / block_size
+  uint32_t block_magic;
   int64_t* slot_mapping;        // [num_rows] (may be NULL)
   int64_t* positions;           // [num_rows] (may be NULL)
   int32_t* cu_seqlens;          // [num_seqs + 1], packed layout only (may be NULL)

@@ -59,8 +59,8 @@ __global__ void __launch_bounds__(256) build_metadata_kernel(MetadataArgs a) {
     const int64_t pos = r < q ? c + r : (L > 0 ? (int64_t)L - 1 : 0);
     int64_t slot = 0;
     if (ok && r < q) {
-      const int64_t bi = pos >> a.block_shift;
-      if (bi < a.bt_width) slot = (int64_t)bt[bi] * a.block_size + (pos & (a.block_size - 1));
+      const int64_t bi = div_bs((uint32_t)pos, a.block_magic, a.block_shift);
+      if (bi < a.bt_width) slot = (int64_t)bt[bi] * a.block_size + (pos - bi * a.block_size);
     }
     if (a.slot_mapping) a.slot_mapping[row] = slot;
     if (a.positions) a.positions[row] = pos;

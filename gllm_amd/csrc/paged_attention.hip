@@ -34,11 +34,6 @@ __device__ __forceinline__ void rope8_bf16(float* x1, float* x2, const float* c,
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 w) { return __builtin_bit_cast(bf16x8, w); }
 
-__device__ __forceinline__ int64_t paged_slot(const AttnArgs& a, const int32_t* bt, int p) {
-  uint32_t blk = (uint32_t)bt[p >> a.block_shift];
-  if (blk >= (uint64_t)a.num_blocks) blk = 0;  // never address outside the pool
-  return (int64_t)blk * a.block_size + (p & (a.block_size - 1));
-}
 
 // ============================================================== decode
 constexpr int kWaves = 8;   // waves per workgroup (both paths; one block size)
@@ -145,8 +140,8 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
   // store does not wait for the others).
   static_assert(Cfg::kMaxBlocks <= 64 * NW, "one block id per thread");
   int32_t* lbid = reinterpret_cast<int32_t*>(lds + NW * Cfg::kVBytes);
-  const int blk0 = kbeg >> a.block_shift;
-  const int nblk = ((kend - 1) >> a.block_shift) - blk0 + 1;
+  const int blk0 = (int)div_bs((uint32_t)kbeg, a.block_magic, a.block_shift);
+  const int nblk = (int)div_bs((uint32_t)(kend - 1), a.block_magic, a.block_shift) - blk0 + 1;
   const int32_t* bt = a.block_table + (int64_t)seq * a.block_table_stride + blk0;
   const uint32_t bid = tid < nblk ? (uint32_t)bt[tid] : 0u;
   const __bf16* qp = (const __bf16*)a.q + qrow * a.q_row_stride + (int64_t)qh * D;
@@ -225,7 +220,6 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
   const char* vc = (const char*)a.v_cache + (int64_t)(head_ok ? kvh : 0) * D * E + 16 * grp;
   const float sl2 = a.scale * kLog2e;
   char* ldsV = lds + wave * Cfg::kVBytes;
-  const uint32_t bmask = a.block_size - 1;
 
   float m = kNegInf, lsum = 0.f;
   f32x4 acc[ND];
@@ -239,7 +233,8 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
     // ring padding (t >= ntw): every lane reads the task's last slot, one
     // cache line per load instead of a whole 16-key tile
     const int key = t < ntw ? min(kbeg + 16 * (ki + KW * t) + n, kend - 1) : kend - 1;
-    const uint32_t slot = (uint32_t)lbid[(key >> a.block_shift) - blk0] * (uint32_t)a.block_size + ((uint32_t)key & bmask);
+    const uint32_t bi = div_bs((uint32_t)key, a.block_magic, a.block_shift);
+    const uint32_t slot = (uint32_t)lbid[bi - blk0] * (uint32_t)a.block_size + ((uint32_t)key - bi * (uint32_t)a.block_size);
     const uint64_t off = (uint64_t)slot * sbytes;
 #pragma unroll
     for (int l = 0; l < NL; ++l) {
@@ -598,7 +593,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   // directly) after the first tiles' copies are issued.
   const int32_t* bt = DENSE ? nullptr : a.block_table + (int64_t)seq * a.block_table_stride;
   constexpr int KB = (Cfg::kBidCache + NT - 1) / NT;
-  const int nbc = DENSE ? 0 : min(((kend_wg - 1) >> a.block_shift) + 1, Cfg::kBidCache);
+  const int nbc = DENSE ? 0 : min((int)div_bs((uint32_t)(kend_wg - 1), a.block_magic, a.block_shift) + 1, Cfg::kBidCache);
   uint32_t lb[KB];
 #pragma unroll
   for (int k = 0; k < KB; ++k) lb[k] = tid + k * NT < nbc ? (uint32_t)bt[tid + k * NT] : 0u;
@@ -657,41 +652,44 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   static_assert(CHD >= 1 && NSEG % NW == 0, "tile / workgroup mismatch");
   constexpr int E = KV8 ? 1 : 2;           // bytes per cached element
   const uint32_t sbytes = (uint32_t)(a.cache_slot_stride * E);
-  const uint32_t bmask = a.block_size - 1;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
-  // Block ids of the DMA rows of the tile starting at key ts (fetched one
-  // tile before the copy is issued, so the copy never waits on LDS).
-  auto dma_bids = [&](int ts, uint32_t (&blk)[CHD]) {
+  // Slots of the DMA rows of the tile starting at key ts: block id from the
+  // LDS cache (or the table past it) times the block size plus the offset in
+  // the block.  Fetched one tile before the copy is issued, so the copy never
+  // waits on LDS.
+  auto dma_bids = [&](int ts, uint32_t (&slot)[CHD]) {
 #pragma unroll
     for (int i = 0; i < CHD; ++i) {
       if (DENSE) {
-        blk[i] = 0;
+        slot[i] = 0;
       } else {
         const int p = min(ts + (i * NW + wave) * RPS + lane / CPR, kend_wg - 1);
-        const int bi = p >> a.block_shift;
-        if (bi < Cfg::kBidCache) {
-          blk[i] = (uint32_t)lbid[bi];
+        const uint32_t bi = div_bs((uint32_t)p, a.block_magic, a.block_shift);
+        uint32_t blk;
+        if (bi < (uint32_t)Cfg::kBidCache) {
+          blk = (uint32_t)lbid[bi];
         } else {
-          blk[i] = (uint32_t)bt[bi];
-          if (blk[i] >= (uint64_t)a.num_blocks) blk[i] = 0;
+          blk = (uint32_t)bt[bi];
+          if (blk >= (uint64_t)a.num_blocks) blk = 0;
         }
+        slot[i] = blk * (uint32_t)a.block_size + ((uint32_t)p - bi * (uint32_t)a.block_size);
       }
     }
   };
   // Source of one lane's 8 elements (logical chunk lc of its row) for copy
-  // instruction i, K (v = 0) or V (v = 1), of the tile at key ts.
-  auto copy_src = [&](int ts, const uint32_t (&blk)[CHD], int i, int v) -> const char* {
+  // instruction i, K (v = 0) or V (v = 1), of the tile at key ts (paged: the
+  // row's slot from dma_bids).
+  auto copy_src = [&](int ts, const uint32_t (&slot)[CHD], int i, int v) -> const char* {
     const int sg = i * NW + wave;
     const int row = sg * RPS + lane / CPR;
     const int lc = (lane % CPR) ^ pf_swz<D>(row);
-    const int p = min(ts + row, kend_wg - 1);
     if (DENSE) {
+      const int p = min(ts + row, kend_wg - 1);
       return (v ? (const char*)a.v + ((int64_t)seq * a.v_batch_stride + (int64_t)p * a.v_row_stride + (int64_t)kvh * D) * 2
                 : (const char*)a.k + ((int64_t)seq * a.k_batch_stride + (int64_t)p * a.k_row_stride + (int64_t)kvh * D) * 2) +
              lc * 16;
     }
-    const uint64_t off = (uint64_t)(blk[i] * (uint32_t)a.block_size + ((uint32_t)p & bmask)) * sbytes +
-                         (uint64_t)kvh * D * E;
+    const uint64_t off = (uint64_t)slot[i] * sbytes + (uint64_t)kvh * D * E;
     return (const char*)(v ? a.v_cache : a.k_cache) + off + lc * 8 * E;
   };
   // One copy instruction into `stage`: bf16 caches go HBM -> LDS directly;
@@ -1004,15 +1002,18 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   // from the table (issued together with the loads above), so they need no
   // trip through LDS and a barrier first; every load so far is waited for
   // here explicitly, so nothing below waits on these copies by accident.
-  uint32_t fbid[TPB][CHD];
+  uint32_t fbid[TPB][CHD], foff[TPB][CHD];
 #pragma unroll
   for (int t = 0; t < TPB; ++t)
 #pragma unroll
     for (int i = 0; i < CHD; ++i) {
       fbid[t][i] = 0u;
+      foff[t][i] = 0u;
       if (!DENSE) {
         const int p = min(t * BN + (i * NW + wave) * RPS + lane / CPR, kend_wg - 1);
-        fbid[t][i] = (uint32_t)bt[p >> a.block_shift];
+        const uint32_t bi = div_bs((uint32_t)p, a.block_magic, a.block_shift);
+        fbid[t][i] = (uint32_t)bt[bi];
+        foff[t][i] = (uint32_t)p - bi * (uint32_t)a.block_size;
       }
     }
   wait_vmcnt<0>();
@@ -1020,8 +1021,10 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   for (int t = 0; t < TPB; ++t)
     if (t < ntiles) {
 #pragma unroll
-      for (int i = 0; i < CHD; ++i)
+      for (int i = 0; i < CHD; ++i) {
         if (fbid[t][i] >= (uint64_t)a.num_blocks) fbid[t][i] = 0u;  // never address outside the pool
+        fbid[t][i] = fbid[t][i] * (uint32_t)a.block_size + foff[t][i];   // the row's slot
+      }
       dma_issue(t * BN, t, fbid[t]);
     }
   if (!DENSE) {

@@ -81,6 +81,8 @@ int gllm_attn_version(void);
  * cu_seqlens[0..num_seqs] (int32, optional) receives the running sums of query_lens.
  * Rows >= num_rows are not written; block-table columns >= block_table_width
  * (and inconsistent lengths) give slot 0.  Any output pointer may be NULL.
+ * block_size: any value in [1, 65536] (the reference's block size is a free
+ * config value).
  * Lengths and table are device pointers: nothing is read back to the host.
  */
 int gllm_build_metadata(const int32_t* block_table, int64_t block_table_stride, int64_t block_table_width,
@@ -179,7 +181,9 @@ int gllm_rope_kv_write(const void* q, void* q_out, const void* k, const void* v,
  * query_lens[i] query rows starting at row i * q_seq_stride of q/out
  * (q_seq_stride = the padded T_q of the reference's [B, T_q, ...] layout), or,
  * if q_seq_stride == 0, packed rows (cumulative query_lens).  seq_lens[i] =
- * context + query length, as llm.py:233-236.  split_tokens = context tokens
+ * context + query length, as llm.py:233-236.  block_size: any value in
+ * [1, 65536] (the kernels divide by it exactly; powers of two are not
+ * required).  split_tokens = context tokens
  * per decode split (multiple of 32) and decode_heads_per_wg = kv heads one
  * decode workgroup serves (1, 2, 4 or 8); 0 lets the planner choose both from
  * the batch and the CU count.  split_tokens == GLLM_SPLIT_BALANCED (-1) plans

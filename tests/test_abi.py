@@ -111,7 +111,8 @@ def test_planner_page_balanced():
     (dict(ql=[0], sl=[5]), _lib.EINVAL),           # empty query
     (dict(ql=[6], sl=[5]), _lib.EINVAL),           # seq shorter than query
     (dict(hq=6, hkv=4), _lib.EINVAL),              # Hq not a multiple of Hkv
-    (dict(bs=12), _lib.EUNSUPPORTED),              # block size not a power of two
+    (dict(bs=0), _lib.EINVAL),                     # block size < 1
+    (dict(bs=65537), _lib.EINVAL),                 # block size above 65536
     (dict(d=96), _lib.EUNSUPPORTED),               # bf16 head_dim
     (dict(split=48), _lib.EINVAL),                 # split not a multiple of 32
     (dict(split=-2), _lib.EINVAL),                 # negative split other than GLLM_SPLIT_BALANCED

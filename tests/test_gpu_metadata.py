@@ -28,6 +28,10 @@ CASES = [
     ([0], [1], 16),                                 # single token
     ([15, 16, 17], [1, 1, 1], 16),                  # positions at block edges
     ([250, 9, 40], [3, 70, 12], 32),                # other block size
+    ([250, 9, 40], [3, 70, 12], 3),                 # block sizes that are not powers of two
+    ([0, 5, 1000], [7, 1, 1], 1),
+    ([100, 47, 0], [20, 1, 30], 24),
+    ([3000, 1, 99], [1, 300, 2], 100),
     ([1000 + 7 * i for i in range(260)], [1] * 256 + [512] * 4, 16),   # config (d)-like batch
 ]
 

@@ -244,6 +244,60 @@ def test_mixed_batch_one_launch():
     assert_close_bf16(out, oracle_paged(b), "mixed")
 
 
+# ------------------------------------------------------------ block sizes
+@pytest.mark.parametrize("bs", [1, 3, 12, 24, 48, 100, 1000])
+@pytest.mark.parametrize("D,split", [(64, 0), (128, 96)])
+def test_any_block_size_mixed(bs, D, split):
+    """Block sizes that are not powers of two (the reference takes any
+    size): one mixed launch with decodes (split and unsplit), prefill chunks
+    with and without context, keys past the prefill kernel's 1024 cached block
+    ids at the small sizes, and a prefill whose context starts mid-block."""
+    print(f"any block size bs={bs} D={D} split={split}", flush=True)
+    ctx = [100, 0, 3500, 513, 7, 1200, 64]
+    ql = [1, 96, 1, 64, 1, 40, 1]
+    b = make_batch(ctx, ql, 32, 8, D, bs=bs)
+    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=32, num_kv_heads=8, head_dim=D,
+                               block_size=bs, dtype=torch.bfloat16, device=DEV, split_tokens=split)
+    assert plan.info["prefill_seqs"] == 3
+    ref = oracle_paged(b)
+    for rep in range(2):
+        out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
+        torch.cuda.synchronize()
+        assert_close_bf16(out, ref, f"bs {bs} rep {rep}")
+
+
+@pytest.mark.parametrize("bs", [1, 3, 24, 100])
+def test_any_block_size_balanced_decode(bs):
+    """Page-balanced decode: segments start on 16-key units, which for these
+    block sizes fall inside blocks."""
+    print(f"balanced decode bs={bs}", flush=True)
+    lens = [1, 9, 16, 47, 130, 511, 2100, 9000]
+    b = make_batch([L - 1 for L in lens], [1] * len(lens), 16, 2, 64, bs=bs)
+    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=16, num_kv_heads=2, head_dim=64,
+                               block_size=bs, dtype=torch.bfloat16, device=DEV, split_tokens=paged.BALANCED)
+    assert plan.info["decode_segments"] > 0
+    ref = oracle_paged(b)
+    for rep in range(2):
+        out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
+        torch.cuda.synchronize()
+        assert_close_bf16(out, ref, f"balanced bs {bs} rep {rep}")
+
+
+@pytest.mark.parametrize("bs", [1, 5, 24])
+@pytest.mark.parametrize("kv", [torch.float32, torch.float8_e4m3fn])
+def test_any_block_size_fp32(bs, kv):
+    print(f"fp32 bs={bs} kv={kv}", flush=True)
+    b = make_batch([0, 63, 300, 1000], [70, 1, 9, 1], 8, 2, 64, bs=bs, dtype=torch.float32)
+    if kv != torch.float32:
+        b.k_cache, b.v_cache = b.k_cache.to(kv), b.v_cache.to(kv)
+    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=8, num_kv_heads=2, head_dim=64,
+                               block_size=bs, dtype=torch.float32, device=DEV)
+    out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
+    torch.cuda.synchronize()
+    d = (out.cpu() - oracle_paged(b)).abs().max().item()
+    assert d < 1e-4, d
+
+
 # ------------------------------------------------------------ fp32 path
 def test_fp32_paged_parity():
     print("fp32 paged", flush=True)
