@@ -204,7 +204,11 @@ def bench_qkv(n_tokens, hidden, Hq, Hkv, D, weight_copies, warmup, reps, dev, se
     vc = torch.zeros_like(kc)
     q_out = torch.empty(n_tokens, Hq, D, dtype=bf, device=dev)
 
-    def fused(w):
+    def fused(w):       # the fused kernel itself
+        paged.qkv_rope_kv_write(x, w[0], w[1], w[2], cos, sin, kc, vc, slots, q_out=q_out, rope_rows=pos,
+                                unfused_from=None)
+
+    def dispatched(w):  # the library entry as callers use it (size-based choice of path)
         paged.qkv_rope_kv_write(x, w[0], w[1], w[2], cos, sin, kc, vc, slots, q_out=q_out, rope_rows=pos)
 
     def unfused(wt):
@@ -216,11 +220,14 @@ def bench_qkv(n_tokens, hidden, Hq, Hkv, D, weight_copies, warmup, reps, dev, se
 
     inner = weight_copies
     tf = statistics.median(graph_reps([lambda w=w: fused(w) for w, _ in ws], warmup, reps, inner)[0])
+    td = statistics.median(graph_reps([lambda w=w: dispatched(w) for w, _ in ws], warmup, reps, inner)[0])
     tu = statistics.median(graph_reps([lambda wt=wt: unfused(wt) for _, wt in ws], warmup, reps, inner)[0])
     flops = 2 * n_tokens * (Hq + 2 * Hkv) * D * hidden
     wbytes = (Hq + 2 * Hkv) * D * hidden * 2
     iobytes = wbytes + n_tokens * hidden * 2 + n_tokens * (Hq + 2 * Hkv) * D * 2
-    return {"tokens": n_tokens, "hidden": hidden, "fused_ms": tf, "unfused_ms": tu, "speedup": tu / tf,
+    return {"tokens": n_tokens, "hidden": hidden, "fused_ms": tf, "dispatched_ms": td, "unfused_ms": tu,
+            "path": "unfused" if n_tokens >= paged.QKV_UNFUSED_FROM else "fused",
+            "speedup": tu / td, "fused_kernel_speedup": tu / tf,
             "tflops": flops / (tf * 1e-3) / 1e12, "mfma_frac": flops / (tf * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
             "gbs": iobytes / (tf * 1e-3) / 1e9, "hbm_frac": iobytes / (tf * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "weight_copies": weight_copies}

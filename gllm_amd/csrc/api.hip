@@ -11,6 +11,8 @@
 #include <string>
 #include <vector>
 
+#include <rocprofiler-sdk-roctx/roctx.h>
+
 #include "../../include/gllm_attn.h"
 #include "launch.h"
 
@@ -40,6 +42,16 @@ int hip_check(hipError_t e, const char* what) {
   if (e == hipSuccess) return ok();
   return fail(GLLM_ATTN_EHIP, "%s: %s", what, hipGetErrorString(e));
 }
+
+// roctx range around each launching entry point (shows in rocprofv3
+// --marker-trace and other ROCm tracers; no cost beyond a call when no tool
+// is attached).
+struct Range {
+  explicit Range(const char* name) { roctxRangePushA(name); }
+  ~Range() { roctxRangePop(); }
+  Range(const Range&) = delete;
+  Range& operator=(const Range&) = delete;
+};
 
 bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 int log2i(int64_t x) {
@@ -265,6 +277,7 @@ int gllm_build_metadata(const int32_t* block_table, int64_t block_table_stride, 
                         const int32_t* seq_lens, const int32_t* query_lens, int32_t num_seqs,
                         int64_t q_seq_stride, int32_t block_size, int64_t* slot_mapping, int64_t* positions,
                         int32_t* cu_seqlens, int64_t num_rows, void* stream) {
+  Range range("gllm_build_metadata");
   if (num_seqs < 0 || num_rows < 0) return fail(GLLM_ATTN_EINVAL, "num_seqs / num_rows < 0");
   if (num_seqs == 0) return ok();
   if (!block_table || !seq_lens || !query_lens) return fail(GLLM_ATTN_EINVAL, "null block_table or lengths");
@@ -295,6 +308,7 @@ int gllm_rope_kv_write(const void* q, void* q_out, const void* k, const void* v,
                        int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
                        int64_t q_out_row_stride, int64_t cache_slot_stride, int64_t num_slots,
                        int32_t dtype, int32_t kv_dtype, void* stream) {
+  Range range("gllm_rope_kv_write");
   if (num_tokens < 0) return fail(GLLM_ATTN_EINVAL, "num_tokens < 0");
   const bool kv = k || v;
   if (!cos || !sin) return fail(GLLM_ATTN_EINVAL, "null cos/sin");
@@ -338,6 +352,7 @@ int gllm_qkv_rope_kv_write(const void* x, int64_t x_row_stride, int64_t num_toke
                            int64_t rope_row_stride, int32_t num_q_heads, int32_t num_kv_heads,
                            int32_t head_dim, int32_t dtype, int32_t kv_dtype, void* workspace,
                            size_t workspace_bytes, void* stream) {
+  Range range("gllm_qkv_rope_kv_write");
   if (num_tokens < 0) return fail(GLLM_ATTN_EINVAL, "num_tokens < 0");
   if (dtype != GLLM_DTYPE_BF16) return fail(GLLM_ATTN_EUNSUPPORTED, "fused QKV projection needs a bf16 model (dtype %d)", dtype);
   if (kv_dtype != GLLM_DTYPE_BF16 && kv_dtype != GLLM_DTYPE_FP8_E4M3)
@@ -421,6 +436,7 @@ int gllm_qkv_rope_kv_write_noalloc(const void* x, int64_t x_row_stride, int64_t 
                                    int64_t tokens_per_seq, const void* cos, const void* sin, const int64_t* rope_rows,
                                    int64_t rope_row_stride, int32_t num_q_heads, int32_t num_kv_heads,
                                    int32_t head_dim, int32_t dtype, int32_t kv_dtype, void* stream) {
+  Range range("gllm_qkv_rope_kv_write_noalloc");
   if (num_tokens < 0 || hidden <= 0 || num_kv_heads <= 0 || num_q_heads <= 0)
     return gllm_qkv_rope_kv_write(x, x_row_stride, num_tokens, hidden, w_q, w_q_row_stride, w_k, w_k_row_stride,
                                   w_v, w_v_row_stride, q_out, q_out_row_stride, rotate_q, k_cache, v_cache,
@@ -702,6 +718,7 @@ int gllm_attn_plan_info(const gllm_attn_plan* p, int64_t* info, int32_t n) {
 }
 
 int gllm_attn_plan_upload(gllm_attn_plan* p, void* workspace, size_t bytes, void* stream) {
+  Range range("gllm_attn_plan_upload");
   if (!p) return fail(GLLM_ATTN_EINVAL, "null plan");
   if (!workspace || bytes < p->ws_bytes)
     return fail(GLLM_ATTN_EINVAL, "workspace of %zu bytes is smaller than the %zu the plan needs", bytes, p->ws_bytes);
@@ -750,6 +767,7 @@ int gllm_paged_attention(const gllm_attn_plan* p, const void* q, int64_t q_row_s
                          int64_t block_table_stride, const void* rope_cos, const void* rope_sin,
                          int64_t rope_row_stride, int32_t rope_mode, float scale, int32_t dtype,
                          int32_t kv_dtype, void* stream) {
+  Range range("gllm_paged_attention");
   if (!p) return fail(GLLM_ATTN_EINVAL, "null plan");
   if (!p->ws) return fail(GLLM_ATTN_EINVAL, "plan was not uploaded (gllm_attn_plan_upload)");
   if (dtype != p->dtype) return fail(GLLM_ATTN_EINVAL, "dtype %d differs from the plan's %d", dtype, p->dtype);
@@ -809,6 +827,7 @@ int gllm_attention_dense(const void* q, int64_t q_row_stride, const void* k, int
                          int64_t out_row_stride, int32_t batch, int32_t q_len, int32_t kv_len,
                          int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
                          int32_t dtype, void* stream) {
+  Range range("gllm_attention_dense");
   if (!q || !k || !v || !bias || !out) return fail(GLLM_ATTN_EINVAL, "null pointer argument");
   if (batch < 0 || q_len < 0 || kv_len < 0) return fail(GLLM_ATTN_EINVAL, "negative size");
   if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads)

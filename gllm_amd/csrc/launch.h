@@ -129,6 +129,7 @@ struct QKVArgs {
   size_t workspace_bytes;
   int32_t cus;                   // compute units (planning)
   int32_t split_chunk, split_count;
+  int32_t vec_stores;            // set by the launcher: rows aligned for 4-element stores
 };
 
 size_t qkv_workspace_bytes(int64_t num_tokens, int hidden, int heads, int head_dim, int cus);

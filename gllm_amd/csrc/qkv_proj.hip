@@ -53,6 +53,14 @@ __host__ __device__ inline QKVGroups qkv_groups(int64_t tiles, int ngroups, int 
   return g;
 }
 
+// Lane n ^ 1 / n ^ 2 of the lane's quad (DPP quad permutes: no LDS trip).
+__device__ __forceinline__ uint32_t quad_xor1(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xf, 0xf, false);   // quad_perm(1,0,3,2)
+}
+__device__ __forceinline__ uint32_t quad_xor2(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xf, 0xf, false);   // quad_perm(2,3,0,1)
+}
+
 // Physical 16-byte chunk of logical chunk c in 64-byte LDS row r: rows
 // r, r+4, r+8, r+12 get the 4 chunk rotations, so 16 consecutive rows
 // reading one logical chunk hit 16 distinct bank groups.
@@ -266,8 +274,38 @@ qkv_rope_write_kernel(QKVArgs a) {
       for (int b = 0; b < NH; ++b)
         rope_pair_bf16(v[b], v[b + NH], bf16_bits_to_f32(csn[j][b] & 0xffffu), bf16_bits_to_f32(csn[j][b] >> 16));
     }
+    // Lanes n .. n + 3 hold head dims 32b + n .. + 3 of the same token: the
+    // quad gathers them (before the row test: every lane of a quad shares the
+    // token) and its first lane stores them with one 4-byte (fp8) or 8-byte
+    // (bf16) store.
+    uint32_t w[NB][2];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      if (KV8 && to_cache) {
+        const uint32_t x = pack_fp8x4(v[b], 0.f, 0.f, 0.f) & 0xffu;
+        const uint32_t y = x | (quad_xor1(x) << 8);
+        w[b][0] = y | (quad_xor2(y) << 16);
+        w[b][1] = 0u;
+      } else {
+        const uint32_t x = pack_bf16x2(v[b], 0.f) & 0xffffu;
+        const uint32_t y = x | (quad_xor1(x) << 16);
+        w[b][0] = y;
+        w[b][1] = quad_xor2(y);
+      }
+    }
     if (dst[j] < 0) continue;
-    if (KV8 && to_cache) {
+    if (a.vec_stores) {                  // rows 4-element aligned (checked on the host)
+      if (n & 3) continue;
+      if (KV8 && to_cache) {
+        char* cp = base + dst[j];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) *reinterpret_cast<uint32_t*>(cp + 32 * b + n) = w[b][0];
+      } else {
+        char* cp = base + dst[j] * 2;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) st8(cp + (32 * b + n) * 2, u32x2{w[b][0], w[b][1]});
+      }
+    } else if (KV8 && to_cache) {
       char* cp = base + dst[j];
 #pragma unroll
       for (int b = 0; b < NB; ++b)
@@ -390,49 +428,77 @@ __global__ void __launch_bounds__(256) qkv_partial_kernel(QKVArgs a) {
   }
 }
 
-// One thread per rotation pair (d, d + D/2) of one (token, head).
+// One thread per 4 rotation pairs (d .. d+3, d+D/2 .. d+D/2+3) of one
+// (token, head): 16-byte partial loads, and 4 values per store (8 bytes bf16,
+// 4 bytes fp8).
 template <int D, bool KV8>
 __global__ void __launch_bounds__(256) qkv_finish_kernel(QKVArgs a) {
   constexpr int PPH = D / 2;              // pairs per head
-  constexpr int HPB = 256 / PPH;          // heads per workgroup
+  constexpr int TPH = PPH / 4;            // threads per head
+  constexpr int HPB = 256 / TPH;          // heads per workgroup
   const int heads = a.num_q_heads + 2 * a.num_kv_heads;
   const int64_t tok = blockIdx.x;
-  const int head = blockIdx.y * HPB + threadIdx.x / PPH;
-  const int d = threadIdx.x % PPH;
+  const int head = blockIdx.y * HPB + threadIdx.x / TPH;
+  const int d = (threadIdx.x % TPH) * 4;
   if (head >= heads) return;
   const int kind = head < a.num_q_heads ? 0 : (head < a.num_q_heads + a.num_kv_heads ? 1 : 2);
   const int h = kind == 0 ? head : (kind == 1 ? head - a.num_q_heads : head - a.num_q_heads - a.num_kv_heads);
   const int64_t F = (int64_t)heads * D;
   const float* ws = a.workspace + tok * F + (int64_t)head * D + d;
-  float x1 = 0.f, x2 = 0.f;
+  f32x4 s1 = {0.f, 0.f, 0.f, 0.f}, s2 = {0.f, 0.f, 0.f, 0.f};
   for (int c = 0; c < a.split_count; ++c) {   // chunk order fixed: deterministic sums
-    x1 += ws[(int64_t)c * a.num_tokens * F];
-    x2 += ws[(int64_t)c * a.num_tokens * F + PPH];
+    s1 += *reinterpret_cast<const f32x4*>(ws + (int64_t)c * a.num_tokens * F);
+    s2 += *reinterpret_cast<const f32x4*>(ws + (int64_t)c * a.num_tokens * F + PPH);
   }
-  round2_bf16(x1, x2);
+  float x1[4], x2[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x1[i] = s1[i];
+    x2[i] = s2[i];
+    round2_bf16(x1[i], x2[i]);
+  }
   // padded rows of the [B, T_q] layout: nothing written, cos/sin not read
   if (a.query_lens && tok % a.tokens_per_seq >= a.query_lens[tok / a.tokens_per_seq]) return;
   if (kind == 1 || (kind == 0 && a.rotate_q)) {
     const int64_t crow = a.rope_rows ? a.rope_rows[tok] : tok;
-    const float c = bf16_bits_to_f32(((const uint16_t*)a.cos)[crow * a.rope_row_stride + d]);
-    const float sn = bf16_bits_to_f32(((const uint16_t*)a.sin)[crow * a.rope_row_stride + d]);
-    rope_pair_bf16(x1, x2, c, sn);
+    const uint16_t* cp = (const uint16_t*)a.cos + crow * a.rope_row_stride + d;
+    const uint16_t* sp = (const uint16_t*)a.sin + crow * a.rope_row_stride + d;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rope_pair_bf16(x1[i], x2[i], bf16_bits_to_f32(cp[i]), bf16_bits_to_f32(sp[i]));
   }
+  // 4 values per store where rows are 4-element aligned (checked on the host)
+  auto put_bf16 = [&](uint16_t* p, const float (&x)[4]) {
+    if (a.vec_stores) {
+      st8(p, u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])});
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = (uint16_t)pack_bf16x2(x[i], 0.f);
+    }
+  };
   if (kind == 0) {
     uint16_t* op = (uint16_t*)a.q_out + tok * a.q_out_row_stride + (int64_t)h * D + d;
-    op[0] = (uint16_t)pack_bf16x2(x1, 0.f);
-    op[PPH] = (uint16_t)pack_bf16x2(x2, 0.f);
+    put_bf16(op, x1);
+    put_bf16(op + PPH, x2);
     return;
   }
   const int64_t slot = a.slot_mapping[tok];
   if (slot < 0 || slot >= a.num_slots) return;
   char* cp = (char*)(kind == 1 ? a.k_cache : a.v_cache) + (slot * a.cache_slot_stride + (int64_t)h * D + d) * (KV8 ? 1 : 2);
   if (KV8) {
-    cp[0] = (char)(pack_fp8x4(x1, 0.f, 0.f, 0.f) & 0xffu);
-    cp[PPH] = (char)(pack_fp8x4(x2, 0.f, 0.f, 0.f) & 0xffu);
+    const uint32_t w1 = pack_fp8x4(x1[0], x1[1], x1[2], x1[3]), w2 = pack_fp8x4(x2[0], x2[1], x2[2], x2[3]);
+    if (a.vec_stores) {
+      *reinterpret_cast<uint32_t*>(cp) = w1;
+      *reinterpret_cast<uint32_t*>(cp + PPH) = w2;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        cp[i] = (char)(w1 >> (8 * i));
+        cp[PPH + i] = (char)(w2 >> (8 * i));
+      }
+    }
   } else {
-    *reinterpret_cast<uint16_t*>(cp) = (uint16_t)pack_bf16x2(x1, 0.f);
-    *reinterpret_cast<uint16_t*>(cp + PPH * 2) = (uint16_t)pack_bf16x2(x2, 0.f);
+    put_bf16(reinterpret_cast<uint16_t*>(cp), x1);
+    put_bf16(reinterpret_cast<uint16_t*>(cp) + PPH, x2);
   }
 }
 
@@ -466,6 +532,11 @@ hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t st) {
   // q heads are the first grid rows; without q_out the grid starts at the k heads
   QKVArgs b = a;
   if (!a.q_out) b.num_q_heads = 0;
+  // 4 consecutive head dims per store: every row start 8-byte aligned (bf16:
+  // element offsets multiple of 4; fp8 cache: 4 bytes)
+  const auto al8 = [](const void* p) { return ((uintptr_t)p & 7) == 0; };
+  b.vec_stores = al8(a.k_cache) && al8(a.v_cache) && a.cache_slot_stride % 4 == 0 &&
+                 (!a.q_out || (al8(a.q_out) && a.q_out_row_stride % 4 == 0));
   const bool kv8 = a.kv_dtype == kFP8;
   int chunk, count;
   qkv_split_plan(a.num_tokens, a.hidden, heads, a.cus, &chunk, &count);
@@ -474,7 +545,8 @@ hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t st) {
     b.split_chunk = chunk;
     b.split_count = count;
     const dim3 g1((unsigned)((a.num_tokens + 63) / 64), (unsigned)heads, (unsigned)count), blk(256);
-    const dim3 g2((unsigned)a.num_tokens, (unsigned)((heads + 256 / (a.head_dim / 2) - 1) / (256 / (a.head_dim / 2))));
+    const int hpb = 256 / (a.head_dim / 8);   // heads per finish workgroup
+    const dim3 g2((unsigned)a.num_tokens, (unsigned)((heads + hpb - 1) / hpb));
     if (a.head_dim == 64) {
       hipLaunchKernelGGL((qkv_partial_kernel<64>), g1, blk, 0, st, b);
       if (kv8) hipLaunchKernelGGL((qkv_finish_kernel<64, true>), g2, blk, 0, st, b);

@@ -8,6 +8,7 @@ import ctypes
 import math
 
 import torch
+import torch.nn.functional as F
 
 from . import _lib
 
@@ -89,11 +90,18 @@ def rope_kv_write(k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torc
         _lib.dtype_code(k.dtype), _lib.dtype_code(k_cache.dtype), _lib.stream_ptr(dev)))
 
 
+# Token count from which qkv_rope_kv_write projects with hipBLASLt (three
+# F.linear calls) and then runs the RoPE + KV write kernel: on MI355X the
+# fused kernel is ahead up to ~1k tokens (3.6x at 64 tokens, 1.03x at 1024)
+# and behind from ~2k (0.90x at 2048, 0.80x at 19679 tokens, 8B shapes).
+QKV_UNFUSED_FROM = 1536
+
+
 def qkv_rope_kv_write(x: torch.Tensor, w_q: torch.Tensor | None, w_k: torch.Tensor, w_v: torch.Tensor,
                       cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                       slot_mapping: torch.Tensor, *, rotate_q: bool = True, q_out: torch.Tensor | None = None,
                       query_lens: torch.Tensor | None = None, rope_rows: torch.Tensor | None = None,
-                      split_k: bool = True):
+                      split_k: bool = True, unfused_from: int | None = QKV_UNFUSED_FROM):
     """Fused ``linear_q/k/v`` + RoPE + KV-cache write of
     ``gllm/model/layers/attention.py:139-161`` (bf16 model).
 
@@ -104,6 +112,9 @@ def qkv_rope_kv_write(x: torch.Tensor, w_q: torch.Tensor | None, w_k: torch.Tens
     ``[N, Hq, D]`` (rotated if ``rotate_q``) or None when ``w_q`` is None.
     ``split_k``: let batches of few tokens split the hidden dimension over
     more workgroups (a cached device workspace); False forces the tile kernel.
+    ``unfused_from``: from this many tokens the projections run as three
+    ``F.linear`` (hipBLASLt) followed by :func:`rope_kv_write`, which is faster
+    there; None always runs the fused kernel.
     """
     hidden = x.shape[-1]
     xs = x.reshape(-1, hidden)
@@ -149,6 +160,16 @@ def qkv_rope_kv_write(x: torch.Tensor, w_q: torch.Tensor | None, w_k: torch.Tens
     rr = None
     if rope_rows is not None:
         rr = rope_rows.reshape(-1).to(torch.int64).contiguous()
+    if unfused_from is not None and n >= unfused_from:
+        k = F.linear(xs, w_k).view(n, Hkv, D)
+        v = F.linear(xs, w_v).view(n, Hkv, D)
+        q = F.linear(xs, w_q).view(n, Hq, D) if w_q is not None else None
+        rotq = q is not None and rotate_q
+        rope_kv_write(k, v, cos, sin, k_cache, v_cache, sm, query_lens=query_lens,
+                      q=q if rotq else None, q_out=q_out.view(n, Hq, D) if rotq else None, rope_rows=rr)
+        if q is not None and not rotate_q:
+            q_out.view(n, Hq, D).copy_(q)
+        return q_out
     lib = _lib.load()
     qrow = q_out.reshape(-1, Hq * D).stride(0) if q_out is not None else 0
     wsb = lib.gllm_qkv_workspace_bytes(n, hidden, max(Hq, 1), Hkv, D, int(w_q is not None)) if split_k else 0

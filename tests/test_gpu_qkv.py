@@ -55,7 +55,7 @@ def _close_bf16(got, want, what, rotated, frac=0.02):
     assert (got != want).float().mean().item() <= frac, f"{what}: {(got != want).float().mean().item():.4f} differ"
 
 
-def _run(n, hidden, Hq, Hkv, D, integer, seed, kv_dtype=BF, rotate_q=True, with_q=True):
+def _run(n, hidden, Hq, Hkv, D, integer, seed, kv_dtype=BF, rotate_q=True, with_q=True, unfused_from=None):
     x, (wq, wk, wv), cos_t, sin_t, pos, slots, ns = _inputs(n, hidden, Hq, Hkv, D, integer, seed)
     sentinel = 3.0
     kc = torch.full((ns, Hkv, D), sentinel, dtype=BF).to(kv_dtype)
@@ -63,7 +63,7 @@ def _run(n, hidden, Hq, Hkv, D, integer, seed, kv_dtype=BF, rotate_q=True, with_
     kc_ref, vc_ref = kc.clone(), vc.clone()
     q = paged.qkv_rope_kv_write(x.to(DEV), wq.to(DEV) if with_q else None, wk.to(DEV), wv.to(DEV),
                                 cos_t.to(DEV), sin_t.to(DEV), kcg := kc.to(DEV), vcg := vc.to(DEV),
-                                slots.to(DEV), rotate_q=rotate_q, rope_rows=pos.to(DEV))
+                                slots.to(DEV), rotate_q=rotate_q, rope_rows=pos.to(DEV), unfused_from=unfused_from)
     torch.cuda.synchronize()
     qr = op.qkv_rope_kv_write(x, wq, wk, wv, cos_t[pos], sin_t[pos], kc_ref, vc_ref, slots, Hkv, D)
     if not rotate_q:
@@ -178,7 +178,7 @@ def test_qkv_split_k_exact_and_matches_tile_path(n, hidden, Hq, Hkv, D):
         kc = torch.full((ns, Hkv, D), 3.0, dtype=BF, device=DEV)
         vc = kc.clone()
         q = paged.qkv_rope_kv_write(x.to(DEV), wq.to(DEV), wk.to(DEV), wv.to(DEV), cos_t.to(DEV), sin_t.to(DEV),
-                                    kc, vc, slots.to(DEV), rope_rows=pos.to(DEV), split_k=split)
+                                    kc, vc, slots.to(DEV), rope_rows=pos.to(DEV), split_k=split, unfused_from=None)
         torch.cuda.synchronize()
         outs.append((q.cpu(), kc.cpu(), vc.cpu()))
     kr = torch.full((ns, Hkv, D), 3.0, dtype=BF)
@@ -201,9 +201,32 @@ def test_qkv_split_k_random_matches_tile_path():
         kc = torch.zeros(ns, Hkv, D, dtype=BF, device=DEV)
         vc = torch.zeros_like(kc)
         q = paged.qkv_rope_kv_write(x.to(DEV), wq.to(DEV), wk.to(DEV), wv.to(DEV), cos_t.to(DEV), sin_t.to(DEV),
-                                    kc, vc, slots.to(DEV), rope_rows=pos.to(DEV), split_k=split)
+                                    kc, vc, slots.to(DEV), rope_rows=pos.to(DEV), split_k=split, unfused_from=None)
         torch.cuda.synchronize()
         res.append((q.cpu(), kc.cpu()[slots], vc.cpu()[slots]))
     _close_bf16(res[0][0], res[1][0], "q", True)
     _close_bf16(res[0][1], res[1][1], "k", True)
     _close_bf16(res[0][2], res[1][2], "v", False)
+
+
+@pytest.mark.parametrize("integer,rotate_q", [(True, True), (False, True), (True, False)])
+def test_qkv_large_batch_unfused_route(integer, rotate_q):
+    """From paged.QKV_UNFUSED_FROM tokens the projections go through F.linear
+    (hipBLASLt) and then the RoPE + KV write kernel: same results as the
+    oracle (exact on small-integer data, within the GEMM's rounding on N(0,1)
+    data), untouched slots keep their sentinel."""
+    n = paged.QKV_UNFUSED_FROM + 300
+    print(f"qkv unfused route n={n} integer={integer} rotate_q={rotate_q}", flush=True)
+    q, qr, kc, vc, kr, vr, slots, ns = _run(n, 256, 8, 2, 128, integer, 41, rotate_q=rotate_q,
+                                            unfused_from=paged.QKV_UNFUSED_FROM)
+    if integer:
+        assert torch.equal(q.cpu().view(torch.int16), qr.view(torch.int16))
+        assert torch.equal(kc.view(torch.int16), kr.view(torch.int16))
+        assert torch.equal(vc.view(torch.int16), vr.view(torch.int16))
+    else:
+        _close_bf16(q, qr, "q", rotate_q)
+        _close_bf16(kc[slots], kr[slots], "k", True)
+        _close_bf16(vc[slots], vr[slots], "v", False)
+    rest = torch.ones(ns, dtype=torch.bool)
+    rest[slots] = False
+    assert bool((kc[rest] == 3.0).all()) and bool((vc[rest] == 3.0).all())
