@@ -154,6 +154,7 @@ struct gllm_attn_plan {
   int32_t num_seqs = 0, Hq = 0, Hkv = 0, D = 0, bs = 0, dtype = 0;
   int32_t split_len = 0, max_q = 0;
   int32_t n_decode_seqs = 0, n_prefill_seqs = 0, heads_per_wg = 8, decode_waves = 8, prefill_waves = 8;
+  bool mfma = false;      // bf16 head dim 64 / 128: the MFMA kernels; otherwise the generic kernel
   int64_t total_rows = 0;
   int64_t n_partials = 0;
   std::vector<SeqInfo> seqs;
@@ -479,14 +480,10 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
                 num_q_heads, num_kv_heads);
   if (block_size <= 0 || block_size > kMaxBlockSize)
     return fail(GLLM_ATTN_EINVAL, "block_size %d must be in [1, %d]", block_size, kMaxBlockSize);
-  if (dtype == GLLM_DTYPE_BF16) {
-    if (head_dim != 64 && head_dim != 128)
-      return fail(GLLM_ATTN_EUNSUPPORTED, "bf16 kernels support head_dim 64 and 128, not %d", head_dim);
-  } else if (dtype == GLLM_DTYPE_F32) {
-    if (head_dim <= 0 || head_dim > 256 || head_dim % 2) return fail(GLLM_ATTN_EUNSUPPORTED, "fp32 head_dim %d", head_dim);
-  } else {
-    return fail(GLLM_ATTN_EUNSUPPORTED, "dtype %d", dtype);
-  }
+  if (dtype != GLLM_DTYPE_BF16 && dtype != GLLM_DTYPE_F32) return fail(GLLM_ATTN_EUNSUPPORTED, "dtype %d", dtype);
+  if (head_dim <= 0 || head_dim > 256 || head_dim % 2)
+    return fail(GLLM_ATTN_EUNSUPPORTED, "head_dim %d (even, at most 256)", head_dim);
+  const bool mfma = dtype == GLLM_DTYPE_BF16 && (head_dim == 64 || head_dim == 128);
   if (split_tokens != GLLM_SPLIT_BALANCED && (split_tokens < 0 || split_tokens % 32))
     return fail(GLLM_ATTN_EINVAL, "split_tokens must be a multiple of 32 or GLLM_SPLIT_BALANCED");
   if (decode_heads_per_wg != 0 && decode_heads_per_wg != 1 && decode_heads_per_wg != 2 &&
@@ -498,7 +495,7 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
   gllm_attn_plan* p = new (std::nothrow) gllm_attn_plan();
   if (!p) return fail(GLLM_ATTN_EINVAL, "out of host memory");
   p->num_seqs = num_seqs; p->Hq = num_q_heads; p->Hkv = num_kv_heads; p->D = head_dim;
-  p->bs = block_size; p->dtype = dtype;
+  p->bs = block_size; p->dtype = dtype; p->mfma = mfma;
   p->seqs.resize(num_seqs);
   int64_t row = 0, decode_tokens = 0;
   for (int i = 0; i < num_seqs; ++i) {
@@ -518,7 +515,7 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
     s.q_len = ql;
     row += ql;
     p->max_q = std::max(p->max_q, ql);
-    if (dtype == GLLM_DTYPE_BF16 && ql * G <= 16) decode_tokens += sl;
+    if (mfma && ql * G <= 16) decode_tokens += sl;
   }
   p->total_rows = q_seq_stride > 0 ? (int64_t)num_seqs * q_seq_stride : row;
   if (p->total_rows > INT32_MAX) {
@@ -526,7 +523,7 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
     return fail(GLLM_ATTN_EINVAL, "too many query rows");
   }
 
-  if (dtype == GLLM_DTYPE_BF16) {
+  if (mfma) {
     int cus = 256;
     int dev = 0;
     hipDeviceProp_t prop;
@@ -815,10 +812,10 @@ int gllm_paged_attention(const gllm_attn_plan* p, const void* q, int64_t q_row_s
   a.decode_waves = p->decode_waves;
   a.prefill_waves = p->prefill_waves;
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == GLLM_DTYPE_BF16)
+  if (p->mfma)
     return hip_check(launch_paged_attention_bf16(a, p->n_prefill_seqs > 0, p->n_decode_seqs > 0, st),
                      "paged attention launch");
-  return hip_check(launch_attention_f32(a, false, p->num_seqs, p->max_q, st), "fp32 attention launch");
+  return hip_check(launch_attention_f32(a, false, p->num_seqs, p->max_q, st), "generic attention launch");
 }
 
 int gllm_attention_dense(const void* q, int64_t q_row_stride, const void* k, int64_t k_batch_stride,
@@ -837,14 +834,9 @@ int gllm_attention_dense(const void* q, int64_t q_row_stride, const void* k, int
   if (k_row_stride < (int64_t)num_kv_heads * head_dim || v_row_stride < (int64_t)num_kv_heads * head_dim)
     return fail(GLLM_ATTN_EINVAL, "k/v row stride too small");
   if (bias_row_stride < kv_len) return fail(GLLM_ATTN_EINVAL, "bias row stride < kv_len");
-  if (dtype == GLLM_DTYPE_BF16) {
-    if (head_dim != 64 && head_dim != 128)
-      return fail(GLLM_ATTN_EUNSUPPORTED, "bf16 kernels support head_dim 64 and 128, not %d", head_dim);
-  } else if (dtype == GLLM_DTYPE_F32) {
-    if (head_dim <= 0 || head_dim > 256) return fail(GLLM_ATTN_EUNSUPPORTED, "fp32 head_dim %d", head_dim);
-  } else {
-    return fail(GLLM_ATTN_EUNSUPPORTED, "dtype %d", dtype);
-  }
+  if (dtype != GLLM_DTYPE_BF16 && dtype != GLLM_DTYPE_F32) return fail(GLLM_ATTN_EUNSUPPORTED, "dtype %d", dtype);
+  if (head_dim <= 0 || head_dim > 256 || head_dim % 2)
+    return fail(GLLM_ATTN_EUNSUPPORTED, "head_dim %d (even, at most 256)", head_dim);
   if (kv_len == 0 && batch * q_len > 0) return fail(GLLM_ATTN_EINVAL, "kv_len == 0 (softmax over no keys)");
   AttnArgs a{};
   if (int rc = fill_common(a, num_q_heads, num_kv_heads, head_dim, scale, dtype, dtype)) return rc;
@@ -854,8 +846,9 @@ int gllm_attention_dense(const void* q, int64_t q_row_stride, const void* k, int
   a.bias = bias; a.bias_batch_stride = bias_batch_stride; a.bias_row_stride = bias_row_stride;
   a.dense_T = kv_len; a.dense_Tq = q_len;
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == GLLM_DTYPE_BF16) return hip_check(launch_dense_attention_bf16(a, batch, q_len, st), "dense attention launch");
-  return hip_check(launch_attention_f32(a, true, batch, q_len, st), "fp32 dense attention launch");
+  if (dtype == GLLM_DTYPE_BF16 && (head_dim == 64 || head_dim == 128))
+    return hip_check(launch_dense_attention_bf16(a, batch, q_len, st), "dense attention launch");
+  return hip_check(launch_attention_f32(a, true, batch, q_len, st), "generic dense attention launch");
 }
 
 }  // extern "C"

@@ -1,9 +1,10 @@
-// fp32 attention (model dtype float32): paged decode/prefill and the dense-bias
-// op.  One wave per (query head, query row, sequence), 64 keys per step, exact
-// online softmax (expf).  This is
-// the path for fp32 models (BASELINE config (a)); the bf16 MFMA kernels are the
-// performance path.  Compiled with -ffp-contract=off so the q rotation rounds
-// each op like the reference (gllm/model/layers/attention.py:105-118).
+// Generic attention: paged decode/prefill and the dense-bias op for fp32
+// models (BASELINE config (a)) and for bf16 models whose head dim the MFMA
+// kernels do not take (not 64 or 128; up to 256).  One wave per (query head,
+// query row, sequence), 64 keys per step, exact online softmax (expf) in
+// fp32.  Compiled with -ffp-contract=off so the q rotation rounds each op
+// like the reference (gllm/model/layers/attention.py:105-118): in fp32, or to
+// bf16 after every op for a bf16 model.
 #include "common.h"
 #include "launch.h"
 
@@ -15,13 +16,23 @@ template <> __device__ __forceinline__ float ldkv<__bf16>(const __bf16* p) { ret
 // fp8 e4m3fn cache: exact widening (the reference's .to(model dtype) after the gather)
 template <> __device__ __forceinline__ float ldkv<fp8e4m3>(const fp8e4m3* p) { return __builtin_amdgcn_cvt_f32_fp8((int)p->bits, 0); }
 
+// model dtype: loads widen exactly; each RoPE op rounds to it
+template <typename QT> __device__ __forceinline__ float rnd(float x);
+template <> __device__ __forceinline__ float rnd<float>(float x) { return x; }
+template <> __device__ __forceinline__ float rnd<__bf16>(float x) { return round_bf16(x); }
+template <typename QT> __device__ __forceinline__ void stq(QT* p, float x);
+template <> __device__ __forceinline__ void stq<float>(float* p, float x) { *p = x; }
+template <> __device__ __forceinline__ void stq<__bf16>(__bf16* p, float x) {
+  *reinterpret_cast<uint16_t*>(p) = (uint16_t)pack_bf16x2(x, 0.f);
+}
+
 // One wave per (query head, query row, sequence).  Keys go 64 at a time: lane
 // j scores key p0 + j against q (q read from LDS, so every lane has all of
 // it), one wave max / sum per chunk updates the exact online softmax (expf),
 // then the lanes switch to the head dims (d = lane + 64 i) and accumulate the
 // chunk's p-weighted V rows, each key's p and slot read out of its lane.  Two
 // memory round trips per 64 keys instead of one per key.
-template <bool DENSE, typename KV>
+template <bool DENSE, typename KV, typename QT>
 __global__ void __launch_bounds__(64) attn_f32_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) float qs[256];
   const int hq = blockIdx.x, r = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
@@ -45,7 +56,7 @@ __global__ void __launch_bounds__(64) attn_f32_kernel(AttnArgs a) {
   const int G = a.num_q_heads / a.num_kv_heads;
   const int kvh = hq / G;
   const int half = D / 2;
-  const float* qp = (const float*)a.q + qrow * a.q_row_stride + (int64_t)hq * D;
+  const QT* qp = (const QT*)a.q + qrow * a.q_row_stride + (int64_t)hq * D;
 
   float acc[4];
 #pragma unroll
@@ -53,16 +64,18 @@ __global__ void __launch_bounds__(64) attn_f32_kernel(AttnArgs a) {
     const int d = lane + 64 * i;
     acc[i] = 0.f;
     if (d < D) {
-      float qv = qp[d];
+      float qv = (float)qp[d];
       if (!DENSE && a.rope_mode != kRopeNone) {
         const int64_t crow = a.rope_mode == kRopeByPosition ? (int64_t)(ctx + r) : qrow;
-        const float* cp = (const float*)a.rope_cos + crow * a.rope_row_stride;
-        const float* sp = (const float*)a.rope_sin + crow * a.rope_row_stride;
+        const QT* cp = (const QT*)a.rope_cos + crow * a.rope_row_stride;
+        const QT* sp = (const QT*)a.rope_sin + crow * a.rope_row_stride;
         if (d < half) {
-          qv = __fsub_rn(__fmul_rn(qp[d], cp[d]), __fmul_rn(qp[d + half], sp[d]));
+          qv = rnd<QT>(__fsub_rn(rnd<QT>(__fmul_rn((float)qp[d], (float)cp[d])),
+                                 rnd<QT>(__fmul_rn((float)qp[d + half], (float)sp[d]))));
         } else {
           const int j = d - half;
-          qv = __fadd_rn(__fmul_rn(qp[j], sp[j]), __fmul_rn(qp[d], cp[j]));
+          qv = rnd<QT>(__fadd_rn(rnd<QT>(__fmul_rn((float)qp[j], (float)sp[j])),
+                                 rnd<QT>(__fmul_rn((float)qp[d], (float)cp[j]))));
         }
       }
       qs[d] = qv;
@@ -77,8 +90,8 @@ __global__ void __launch_bounds__(64) attn_f32_kernel(AttnArgs a) {
                           : (const KV*)a.v_cache + (int64_t)kvh * D;
   const int64_t kstride = DENSE ? a.k_row_stride : a.cache_slot_stride;
   const int64_t vstride = DENSE ? a.v_row_stride : a.cache_slot_stride;
-  const float* brow = DENSE ? (const float*)a.bias + (int64_t)b * a.bias_batch_stride + (int64_t)r * a.bias_row_stride
-                            : nullptr;
+  const QT* brow = DENSE ? (const QT*)a.bias + (int64_t)b * a.bias_batch_stride + (int64_t)r * a.bias_row_stride
+                         : nullptr;
   float m = kNegInf, l = 0.f;
   for (int p0 = 0; p0 < nkeys; p0 += 64) {
     const int p = p0 + lane;
@@ -107,7 +120,7 @@ __global__ void __launch_bounds__(64) attn_f32_kernel(AttnArgs a) {
       }
       for (; d < D; ++d) dot += qs[d] * ldkv<KV>(kp + d);   // head dims not a multiple of 4
       s = dot * a.scale;
-      if (DENSE) s += brow[p];
+      if (DENSE) s += (float)brow[p];
     }
     float cm = s;
 #pragma unroll
@@ -149,25 +162,33 @@ __global__ void __launch_bounds__(64) attn_f32_kernel(AttnArgs a) {
     }
     m = mn;
   }
-  float* op = (float*)a.out + qrow * a.out_row_stride + (int64_t)hq * D;
+  QT* op = (QT*)a.out + qrow * a.out_row_stride + (int64_t)hq * D;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int d = lane + 64 * i;
-    if (d < D) op[d] = acc[i] / l;  // l == 0 (every key masked) gives NaN, as torch's softmax
+    if (d < D) stq<QT>(op + d, acc[i] / l);  // l == 0 (every key masked) gives NaN, as torch's softmax
   }
 }
 
 hipError_t launch_attention_f32(const AttnArgs& a, bool dense, int B, int max_q, hipStream_t st) {
   if (B == 0 || max_q == 0) return hipSuccess;
   dim3 grid(a.num_q_heads, max_q, B), block(64);
-  if (dense)
-    hipLaunchKernelGGL((attn_f32_kernel<true, float>), grid, block, 0, st, a);
-  else if (a.kv_dtype == kF32)
-    hipLaunchKernelGGL((attn_f32_kernel<false, float>), grid, block, 0, st, a);
-  else if (a.kv_dtype == kFP8)
-    hipLaunchKernelGGL((attn_f32_kernel<false, fp8e4m3>), grid, block, 0, st, a);
-  else
-    hipLaunchKernelGGL((attn_f32_kernel<false, __bf16>), grid, block, 0, st, a);
+  if (a.dtype == kBF16) {                 // bf16 model (head dims the MFMA kernels do not take)
+    if (dense)
+      hipLaunchKernelGGL((attn_f32_kernel<true, __bf16, __bf16>), grid, block, 0, st, a);
+    else if (a.kv_dtype == kFP8)
+      hipLaunchKernelGGL((attn_f32_kernel<false, fp8e4m3, __bf16>), grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL((attn_f32_kernel<false, __bf16, __bf16>), grid, block, 0, st, a);
+  } else if (dense) {
+    hipLaunchKernelGGL((attn_f32_kernel<true, float, float>), grid, block, 0, st, a);
+  } else if (a.kv_dtype == kF32) {
+    hipLaunchKernelGGL((attn_f32_kernel<false, float, float>), grid, block, 0, st, a);
+  } else if (a.kv_dtype == kFP8) {
+    hipLaunchKernelGGL((attn_f32_kernel<false, fp8e4m3, float>), grid, block, 0, st, a);
+  } else {
+    hipLaunchKernelGGL((attn_f32_kernel<false, __bf16, float>), grid, block, 0, st, a);
+  }
   return hipGetLastError();
 }
 

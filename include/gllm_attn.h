@@ -222,8 +222,9 @@ int gllm_attn_plan_destroy(gllm_attn_plan* plan);
  * Query head h reads kv head h / (num_q_heads / num_kv_heads).
  * rope_mode != NONE rotates q on load (bit-identical to apply_rope).
  * bf16 model dtype runs the MFMA kernels (head_dim 64 or 128) over a bf16 or
- * fp8 e4m3fn cache; f32 model dtype runs the fp32 kernel (kv f32, bf16 or
- * fp8 e4m3fn).  An fp8 cache is read as the reference reads it: each value
+ * fp8 e4m3fn cache, and a generic kernel (fp32 arithmetic, bf16 in and out)
+ * for any other even head_dim up to 256; f32 model dtype runs the generic
+ * kernel (kv f32, bf16 or fp8 e4m3fn).  An fp8 cache is read as the reference reads it: each value
  * widened exactly to the model dtype (attention.py:169-170's .to(q.dtype)).
  * Returns after enqueueing on `stream`.
  */

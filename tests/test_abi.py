@@ -113,7 +113,8 @@ def test_planner_page_balanced():
     (dict(hq=6, hkv=4), _lib.EINVAL),              # Hq not a multiple of Hkv
     (dict(bs=0), _lib.EINVAL),                     # block size < 1
     (dict(bs=65537), _lib.EINVAL),                 # block size above 65536
-    (dict(d=96), _lib.EUNSUPPORTED),               # bf16 head_dim
+    (dict(d=97), _lib.EUNSUPPORTED),               # odd head_dim
+    (dict(d=258), _lib.EUNSUPPORTED),              # head_dim above 256
     (dict(split=48), _lib.EINVAL),                 # split not a multiple of 32
     (dict(split=-2), _lib.EINVAL),                 # negative split other than GLLM_SPLIT_BALANCED
     (dict(hw=3), _lib.EINVAL),                     # heads per decode workgroup

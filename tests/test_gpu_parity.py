@@ -298,6 +298,45 @@ def test_any_block_size_fp32(bs, kv):
     assert d < 1e-4, d
 
 
+# ------------------------------------------------------------ other head dims (bf16)
+@pytest.mark.parametrize("D", [32, 80, 96, 256])
+@pytest.mark.parametrize("kv", [torch.bfloat16, torch.float8_e4m3fn])
+def test_bf16_other_head_dims(D, kv):
+    """bf16 models with a head dim the MFMA kernels do not take run the
+    generic kernel (fp32 arithmetic, q rotated on load with bf16 rounding per
+    op): mixed decode + prefill batch, bf16 or fp8 cache, same bar as the
+    MFMA paths."""
+    print(f"bf16 head dim D={D} kv={kv}", flush=True)
+    b = make_batch([0, 63, 300, 1000, 5], [70, 1, 9, 1, 33], 16, 4, D, theta=10000.0)
+    if kv != torch.bfloat16:
+        b.k_cache, b.v_cache = b.k_cache.to(kv), b.v_cache.to(kv)
+    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=16, num_kv_heads=4, head_dim=D,
+                               block_size=16, dtype=torch.bfloat16, device=DEV)
+    out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table,
+                                rope=(b.cos, b.sin, "position"))
+    torch.cuda.synchronize()
+    pos = torch.cat([torch.arange(c, c + q) for c, q in zip(b.ctx_lens, b.q_lens)])
+    q_rot = orope.apply_rope(b.q.cpu().unsqueeze(0), b.cos.cpu()[pos].unsqueeze(0), b.sin.cpu()[pos].unsqueeze(0))[0]
+    assert_close_bf16(out, oracle_paged(b, q_rot), f"D={D}")
+
+
+@pytest.mark.parametrize("D", [48, 96])
+def test_bf16_dense_op_other_head_dims(D):
+    """reference_attention (dense bias op) for bf16 at other head dims."""
+    print(f"bf16 dense D={D}", flush=True)
+    g = torch.Generator().manual_seed(D)
+    B, Tq, T, Hq, Hkv = 2, 24, 40, 4, 2
+    q = torch.randn(B, Tq, Hq, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, T, Hkv, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, T, Hkv, D, generator=g).to(torch.bfloat16)
+    bias = torch.where(torch.rand(B, Tq, T, generator=g) < 0.2, float("-inf"), 0.0).to(torch.bfloat16)
+    bias[..., 0] = 0.0
+    out = gllm_amd.reference_attention(q.to(DEV), k.to(DEV), v.to(DEV), bias.to(DEV))
+    torch.cuda.synchronize()
+    ref = oa.reference_attention(q.float(), k.float(), v.float(), bias.float())
+    assert_close_bf16(out, ref, f"dense D={D}")
+
+
 # ------------------------------------------------------------ fp32 path
 def test_fp32_paged_parity():
     print("fp32 paged", flush=True)
@@ -524,7 +563,7 @@ def test_attention_layer_forward_real_weights(dtype):
 def test_errors_are_raised():
     print("errors", flush=True)
     with pytest.raises(NotImplementedError):
-        paged.AttentionPlan([1], [10], num_q_heads=8, num_kv_heads=2, head_dim=96, block_size=16,
+        paged.AttentionPlan([1], [10], num_q_heads=8, num_kv_heads=2, head_dim=320, block_size=16,
                             dtype=torch.bfloat16, device=DEV)
     with pytest.raises(ValueError):
         paged.AttentionPlan([5], [3], num_q_heads=8, num_kv_heads=2, head_dim=64, block_size=16,
