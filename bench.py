@@ -313,6 +313,33 @@ def bench_decode_step(dtype, warmup, reps, dev):
             "speedup": eager / graph}
 
 
+def progress(what: str) -> None:
+    """One line per stage on stderr (the JSON result line stays alone on stdout)."""
+    print(f"[bench] {what}", file=sys.stderr, flush=True)
+
+
+def bench_box_ceilings(dev, warmup, reps):
+    """What this box's library kernels reach on plain patterns, as context
+    for the roofline fractions (not the peaks they are priced against): a
+    device copy of 2 GiB (torch's copy kernel; bytes read + written) and a
+    bf16 8192^3 GEMM (torch.mm -> hipBLASLt)."""
+    src = torch.empty(1 << 30, dtype=torch.bfloat16, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    per, _ = graph_reps([lambda: dst.copy_(src)], warmup, reps, 1)
+    copy_ms = statistics.median(per)
+    del src, dst
+    a = torch.randn(8192, 8192, device=dev).to(torch.bfloat16)
+    bm = torch.randn(8192, 8192, device=dev).to(torch.bfloat16)
+    per, _ = graph_reps([lambda: torch.mm(a, bm)], warmup, max(5, reps // 4), 1)
+    gemm_ms = statistics.median(per)
+    del a, bm
+    torch.cuda.empty_cache()
+    cb = 2 * (2 << 30)
+    return {"copy_2gib_gbs": cb / (copy_ms * 1e-3) / 1e9, "copy_frac_of_hbm_peak": cb / (copy_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "gemm_bf16_8192_tflops": 2 * 8192 ** 3 / (gemm_ms * 1e-3) / 1e12,
+            "gemm_frac_of_mfma_peak": 2 * 8192 ** 3 / (gemm_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
+
+
 def bench_plan_host(b: workloads.PagedBatch, reps: int, dev):
     """Host cost of one engine step's plan (what plan_for pays once per step):
     create (planner + pinned staging from the library's pool), device
@@ -436,6 +463,7 @@ def main():
     ap.add_argument("--hw", type=int, default=0, help="kv heads per decode workgroup (0 = planner's choice)")
     ap.add_argument("--copies", type=int, default=4, help="KV pool copies rotated for config (b)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-ceilings", action="store_true", help="skip the copy / GEMM reference measurements")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a plain 256 MiB device copy (known bytes) for counter calibration")
     args = ap.parse_args()
@@ -452,6 +480,7 @@ def main():
     head = None
     head_cpu = None
     if "d" in cfgs:
+        progress("config (d)")
         d = workloads.config_d()
         head, xd, _ = bench_paged(d, 1, args.warmup, reps, 4, dev, args.split, args.hw)
         head["roofline"] = roofline_hbm(head["bytes_per_launch"], head["ms_per_step"], "mixed_8b")
@@ -469,6 +498,7 @@ def main():
         extra["decode_8b"] = r
         torch.cuda.empty_cache()
     if "c" in cfgs:
+        progress("config (c)")
         c = workloads.config_c()
         r, xc, _ = bench_paged(c, 2, args.warmup, reps, 4, dev, eager=False, rope=True)
         r["roofline"] = roofline_mfma(r["flops_per_launch"], r["ms_per_step"], "prefill_8b")
@@ -483,6 +513,7 @@ def main():
         extra["qkv_prefill_8b"] = bench_qkv(c.rows, 4096, 32, 8, 128, 2, args.warmup, max(10, reps // 3), dev)
         torch.cuda.empty_cache()
     if "b" in cfgs:
+        progress("config (b)")
         b = workloads.config_b()
         r, xb, _ = bench_paged(b, args.copies, args.warmup, reps, 2 * args.copies, dev, args.split, args.hw)
         r["roofline"] = roofline_hbm(r["bytes_per_launch"], r["ms_per_step"], "decode_1b")
@@ -504,6 +535,7 @@ def main():
         extra["qkv_decode_1b"] = bench_qkv(64, 2048, 32, 8, 64, 24, args.warmup, max(10, reps // 3), dev)
         torch.cuda.empty_cache()
     if "a" in cfgs:
+        progress("config (a)")
         # config (a)'s decode step: 16 layers x (RoPE + KV write, paged attention), eager vs one HIP graph
         extra["decode_step_1b_fp32"] = bench_decode_step(torch.float32, args.warmup, max(10, reps // 2), dev)
         extra["decode_step_1b_bf16"] = bench_decode_step(torch.bfloat16, args.warmup, max(10, reps // 2), dev)
@@ -511,6 +543,7 @@ def main():
         extra["plan_host_decode_1b"] = bench_plan_host(workloads.config_b(), 50, dev)
         torch.cuda.empty_cache()
     if "e" in cfgs:
+        progress("config (e)")
         e = workloads.config_e()
         r, xe, _ = bench_paged(e, 1, args.warmup, max(10, reps // 2), 1, dev, args.split, args.hw, eager=False)
         r["roofline"] = roofline_hbm(r["bytes_per_launch"], r["ms_per_step"], "long_decode_70b")
@@ -520,6 +553,9 @@ def main():
         extra["long_decode_70b"] = r
         del xe
         torch.cuda.empty_cache()
+    if not args.no_ceilings:
+        progress("copy / GEMM reference")
+        extra["box_ceilings"] = bench_box_ceilings(dev, args.warmup, max(10, reps // 3))
     if args.calibrate:
         src = torch.empty(128 << 20, dtype=torch.bfloat16, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
