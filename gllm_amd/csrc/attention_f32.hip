@@ -26,16 +26,21 @@ template <> __device__ __forceinline__ void stq<__bf16>(__bf16* p, float x) {
   *reinterpret_cast<uint16_t*>(p) = (uint16_t)pack_bf16x2(x, 0.f);
 }
 
-// One wave per (query head, query row, sequence).  Keys go 64 at a time: lane
-// j scores key p0 + j against q (q read from LDS, so every lane has all of
-// it), one wave max / sum per chunk updates the exact online softmax (expf),
-// then the lanes switch to the head dims (d = lane + 64 i) and accumulate the
-// chunk's p-weighted V rows, each key's p and slot read out of its lane.  Two
-// memory round trips per 64 keys instead of one per key.
+// One 4-wave workgroup per (query head, query row, sequence).  Keys go 64 at
+// a time, chunk c to wave c % 4: lane j scores key p0 + j against q (q read
+// from LDS, so every lane has all of it), one wave max / sum per chunk
+// updates the wave's exact online softmax (expf), then the lanes switch to
+// the head dims (d = lane + 64 i) and accumulate the chunk's p-weighted V
+// rows, 32 keys' rows loaded at once, each key's p and slot read out of its
+// lane.  The four waves' (max, sum, acc) merge through LDS at the end.
 template <bool DENSE, typename KV, typename QT>
-__global__ void __launch_bounds__(64) attn_f32_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
+  constexpr int NWV = 4;                  // waves per workgroup
+  constexpr int VB = 32;                  // V rows per batch of loads
   __shared__ __attribute__((aligned(16))) float qs[256];
-  const int hq = blockIdx.x, r = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
+  __shared__ float mrg[NWV][2 + 256];     // per wave: max, sum, acc[D]
+  const int hq = blockIdx.x, r = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int D = a.head_dim;
   int ctx, qlen, L;
   int64_t qrow;
@@ -58,28 +63,22 @@ __global__ void __launch_bounds__(64) attn_f32_kernel(AttnArgs a) {
   const int half = D / 2;
   const QT* qp = (const QT*)a.q + qrow * a.q_row_stride + (int64_t)hq * D;
 
-  float acc[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int d = lane + 64 * i;
-    acc[i] = 0.f;
-    if (d < D) {
-      float qv = (float)qp[d];
-      if (!DENSE && a.rope_mode != kRopeNone) {
-        const int64_t crow = a.rope_mode == kRopeByPosition ? (int64_t)(ctx + r) : qrow;
-        const QT* cp = (const QT*)a.rope_cos + crow * a.rope_row_stride;
-        const QT* sp = (const QT*)a.rope_sin + crow * a.rope_row_stride;
-        if (d < half) {
-          qv = rnd<QT>(__fsub_rn(rnd<QT>(__fmul_rn((float)qp[d], (float)cp[d])),
-                                 rnd<QT>(__fmul_rn((float)qp[d + half], (float)sp[d]))));
-        } else {
-          const int j = d - half;
-          qv = rnd<QT>(__fadd_rn(rnd<QT>(__fmul_rn((float)qp[j], (float)sp[j])),
-                                 rnd<QT>(__fmul_rn((float)qp[d], (float)cp[j]))));
-        }
+  for (int d = tid; d < D; d += 64 * NWV) {
+    float qv = (float)qp[d];
+    if (!DENSE && a.rope_mode != kRopeNone) {
+      const int64_t crow = a.rope_mode == kRopeByPosition ? (int64_t)(ctx + r) : qrow;
+      const QT* cp = (const QT*)a.rope_cos + crow * a.rope_row_stride;
+      const QT* sp = (const QT*)a.rope_sin + crow * a.rope_row_stride;
+      if (d < half) {
+        qv = rnd<QT>(__fsub_rn(rnd<QT>(__fmul_rn((float)qp[d], (float)cp[d])),
+                               rnd<QT>(__fmul_rn((float)qp[d + half], (float)sp[d]))));
+      } else {
+        const int j = d - half;
+        qv = rnd<QT>(__fadd_rn(rnd<QT>(__fmul_rn((float)qp[j], (float)sp[j])),
+                               rnd<QT>(__fmul_rn((float)qp[d], (float)cp[j]))));
       }
-      qs[d] = qv;
     }
+    qs[d] = qv;
   }
   __syncthreads();
   const int nkeys = DENSE ? L : ctx + r + 1;
@@ -93,7 +92,8 @@ __global__ void __launch_bounds__(64) attn_f32_kernel(AttnArgs a) {
   const QT* brow = DENSE ? (const QT*)a.bias + (int64_t)b * a.bias_batch_stride + (int64_t)r * a.bias_row_stride
                          : nullptr;
   float m = kNegInf, l = 0.f;
-  for (int p0 = 0; p0 < nkeys; p0 += 64) {
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int p0 = 64 * wave; p0 < nkeys; p0 += 64 * NWV) {
     const int p = p0 + lane;
     const bool valid = p < nkeys;
     // row of key p in k (dense) or in the paged cache
@@ -113,7 +113,8 @@ __global__ void __launch_bounds__(64) attn_f32_kernel(AttnArgs a) {
       const KV* kp = kbase + row * kstride;
       float dot = 0.f;
       int d = 0;
-      for (; d + 4 <= D; d += 4) {
+#pragma unroll 16
+      for (; d + 4 <= D; d += 4) {                     // unrolled: the row's loads are in flight together
         const f32x4 qv = *reinterpret_cast<const f32x4*>(qs + d);
         dot += qv[0] * ldkv<KV>(kp + d) + qv[1] * ldkv<KV>(kp + d + 1) + qv[2] * ldkv<KV>(kp + d + 2) +
                qv[3] * ldkv<KV>(kp + d + 3);
@@ -137,12 +138,12 @@ __global__ void __launch_bounds__(64) attn_f32_kernel(AttnArgs a) {
     for (int i = 0; i < 4; ++i) acc[i] *= alpha;
     const int nk = min(64, nkeys - p0);
     const int rlo = (int)(uint32_t)row, rhi = (int)((uint64_t)row >> 32);
-    // 8 keys' V rows in flight at a time (keys past the chunk re-read its last
+    // VB keys' V rows loaded at once (keys past the chunk re-read its last
     // row with weight 0), summed in key order
-    for (int j0 = 0; j0 < nk; j0 += 8) {
-      float pj[8], vv[8][4];
+    for (int j0 = 0; j0 < nk; j0 += VB) {
+      float pj[VB], vv[VB][4];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < VB; ++u) {
         const int j = min(j0 + u, nk - 1);
         const float pe = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(e), j));
         pj[u] = j0 + u < nk ? pe : 0.f;
@@ -156,23 +157,50 @@ __global__ void __launch_bounds__(64) attn_f32_kernel(AttnArgs a) {
         }
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
+      for (int u = 0; u < VB; ++u)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] += pj[u] * vv[u][i];
     }
     m = mn;
   }
+  // merge the waves' states (exact LSE merge; a wave without keys has
+  // m = -inf and weight 0)
+  if (lane == 0) {
+    mrg[wave][0] = m;
+    mrg[wave][1] = l;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = lane + 64 * i;
+    if (d < D) mrg[wave][2 + d] = acc[i];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float M = kNegInf;
+#pragma unroll
+  for (int w = 0; w < NWV; ++w) M = fmaxf(M, mrg[w][0]);
+  float wt[NWV], lt = 0.f;
+#pragma unroll
+  for (int w = 0; w < NWV; ++w) {
+    wt[w] = mrg[w][0] == kNegInf ? 0.f : expf(mrg[w][0] - M);
+    lt += wt[w] * mrg[w][1];
+  }
   QT* op = (QT*)a.out + qrow * a.out_row_stride + (int64_t)hq * D;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int d = lane + 64 * i;
-    if (d < D) stq<QT>(op + d, acc[i] / l);  // l == 0 (every key masked) gives NaN, as torch's softmax
+    if (d < D) {
+      float o = 0.f;
+#pragma unroll
+      for (int w = 0; w < NWV; ++w) o += wt[w] * mrg[w][2 + d];
+      stq<QT>(op + d, o / lt);   // lt == 0 (every key masked) gives NaN, as torch's softmax
+    }
   }
 }
 
 hipError_t launch_attention_f32(const AttnArgs& a, bool dense, int B, int max_q, hipStream_t st) {
   if (B == 0 || max_q == 0) return hipSuccess;
-  dim3 grid(a.num_q_heads, max_q, B), block(64);
+  dim3 grid(a.num_q_heads, max_q, B), block(256);
   if (a.dtype == kBF16) {                 // bf16 model (head dims the MFMA kernels do not take)
     if (dense)
       hipLaunchKernelGGL((attn_f32_kernel<true, __bf16, __bf16>), grid, block, 0, st, a);
