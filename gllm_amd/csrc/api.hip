@@ -588,11 +588,7 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
     p->heads_per_wg = best_hw;
     p->decode_waves = best_nw;
     // Prefill: 8-wave workgroups, one per CU (4-stage K/V ring in LDS).
-    int pw = 8;
-    if (ndec == 0) {
-      const char* e = std::getenv("GLLM_PREFILL_WAVES");
-      if (e && std::atoi(e) == 4) pw = 4;
-    }
+    const int pw = 8;
     p->prefill_waves = pw;
     const int hgroups = (num_kv_heads + best_hw - 1) / best_hw;
     const int64_t S = best_S;

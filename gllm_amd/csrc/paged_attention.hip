@@ -1158,16 +1158,13 @@ decode_balanced_kernel(AttnArgs a) {
   }
 }
 
-// Prefill items only.  NW = 8: one workgroup per CU, a 4-stage ring; NW = 4:
-// two workgroups per CU (one wave per SIMD each), a 2-stage ring, so one
-// workgroup's prologue overlaps the other's main loop.
-template <int D, bool KV8, int NW>
-__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
+// Prefill items only: one 8-wave workgroup per CU, a 4-stage ring.
+template <int D, bool KV8>
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2)))
 prefill_bf16_kernel(AttnArgs a) {
-  constexpr int NS = NW == 8 ? kPrefillStages : 2;
-  __shared__ __attribute__((aligned(16))) char lds[PrefillCfg<D, NS>::kLdsBytes];
+  __shared__ __attribute__((aligned(16))) char lds[PrefillCfg<D, kPrefillStages>::kLdsBytes];
   const WorkItem it = a.items[blockIdx.x];
-  prefill_wg<D, false, NW, NS, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
+  prefill_wg<D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
 }
 
 template <int D>
@@ -1188,10 +1185,7 @@ static void launch_paged_hk(const AttnArgs& a, bool pf, bool dc, hipStream_t st)
     if constexpr (HW * KW == kWaves)
       hipLaunchKernelGGL((paged_attn_bf16_kernel<D, true, true, HW, KW, KV8>), grid, dim3(64 * kWaves), 0, st, a);
   } else if (pf) {
-    if (a.prefill_waves == 4)
-      hipLaunchKernelGGL((prefill_bf16_kernel<D, KV8, 4>), grid, dim3(256), 0, st, a);
-    else
-      hipLaunchKernelGGL((prefill_bf16_kernel<D, KV8, kWaves>), grid, dim3(64 * kWaves), 0, st, a);
+    hipLaunchKernelGGL((prefill_bf16_kernel<D, KV8>), grid, dim3(64 * kWaves), 0, st, a);
   } else {
     hipLaunchKernelGGL((paged_attn_bf16_kernel<D, false, true, HW, KW, KV8>), grid, dim3(64 * HW * KW), 0, st, a);
   }
@@ -1217,7 +1211,7 @@ static hipError_t launch_paged_d(const AttnArgs& a, bool pf, bool dc, hipStream_
     if (pf || nw != kWaves) return hipErrorInvalidValue;
     return launch_decode_balanced<D, KV8>(a, st);
   }
-  if (pf && ((a.prefill_waves != kWaves && (dc || a.prefill_waves != 4)) || (dc && nw != kWaves)))
+  if (pf && (a.prefill_waves != kWaves || (dc && nw != kWaves)))
     return hipErrorInvalidValue;
   if (nw == 8) {
     switch (hw) {

@@ -328,6 +328,18 @@ qkv_rope_write_kernel(QKVArgs a) {
 // [chunk][token][head * D + d]); qkv_finish_kernel sums the chunks in fixed
 // order (deterministic), rounds like F.linear and does the RoPE and the
 // stores exactly as the tile kernel's epilogue.
+// s_waitcnt vmcnt(after * IPS) for a run-time `after` in [0, M].
+template <int IPS, int M>
+__device__ __forceinline__ void wait_stages(int after) {
+  if constexpr (M >= 0) {
+    if (after >= M) {
+      wait_vmcnt<M * IPS>();
+      return;
+    }
+    wait_stages<IPS, M - 1>(after);
+  }
+}
+
 template <int D>
 __global__ void __launch_bounds__(256) qkv_partial_kernel(QKVArgs a) {
   constexpr int TM = 64;                  // tokens per workgroup (waves: 2 token blocks x 2 output halves)
@@ -391,13 +403,7 @@ __global__ void __launch_bounds__(256) qkv_partial_kernel(QKVArgs a) {
   for (int s = 0; s < NS - 1; ++s)
     if (s < nk) dma(s, s);
   for (int ks = 0; ks < nk; ++ks) {
-    const int after = min(NS - 2, nk - 1 - ks);
-    if (after >= 2)
-      wait_vmcnt<2 * IPS>();
-    else if (after == 1)
-      wait_vmcnt<IPS>();
-    else
-      wait_vmcnt<0>();
+    wait_stages<IPS, NS - 2>(min(NS - 2, nk - 1 - ks));   // stage ks in; later stages may still fly
     __syncthreads();
     if (ks + NS - 1 < nk) dma(ks + NS - 1, (ks + NS - 1) % NS);
     if (wact) {
@@ -432,10 +438,10 @@ __global__ void __launch_bounds__(256) qkv_partial_kernel(QKVArgs a) {
 // (token, head): 16-byte partial loads, and 4 values per store (8 bytes bf16,
 // 4 bytes fp8).
 template <int D, bool KV8>
-__global__ void __launch_bounds__(256) qkv_finish_kernel(QKVArgs a) {
+__global__ void __launch_bounds__(64) qkv_finish_kernel(QKVArgs a) {
   constexpr int PPH = D / 2;              // pairs per head
   constexpr int TPH = PPH / 4;            // threads per head
-  constexpr int HPB = 256 / TPH;          // heads per workgroup
+  constexpr int HPB = 64 / TPH;           // heads per (one-wave) workgroup
   const int heads = a.num_q_heads + 2 * a.num_kv_heads;
   const int64_t tok = blockIdx.x;
   const int head = blockIdx.y * HPB + threadIdx.x / TPH;
@@ -545,16 +551,16 @@ hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t st) {
     b.split_chunk = chunk;
     b.split_count = count;
     const dim3 g1((unsigned)((a.num_tokens + 63) / 64), (unsigned)heads, (unsigned)count), blk(256);
-    const int hpb = 256 / (a.head_dim / 8);   // heads per finish workgroup
-    const dim3 g2((unsigned)a.num_tokens, (unsigned)((heads + hpb - 1) / hpb));
+    const int hpb = 64 / (a.head_dim / 8);    // heads per finish workgroup (one wave)
+    const dim3 g2((unsigned)a.num_tokens, (unsigned)((heads + hpb - 1) / hpb)), blk2(64);
     if (a.head_dim == 64) {
       hipLaunchKernelGGL((qkv_partial_kernel<64>), g1, blk, 0, st, b);
-      if (kv8) hipLaunchKernelGGL((qkv_finish_kernel<64, true>), g2, blk, 0, st, b);
-      else hipLaunchKernelGGL((qkv_finish_kernel<64, false>), g2, blk, 0, st, b);
+      if (kv8) hipLaunchKernelGGL((qkv_finish_kernel<64, true>), g2, blk2, 0, st, b);
+      else hipLaunchKernelGGL((qkv_finish_kernel<64, false>), g2, blk2, 0, st, b);
     } else if (a.head_dim == 128) {
       hipLaunchKernelGGL((qkv_partial_kernel<128>), g1, blk, 0, st, b);
-      if (kv8) hipLaunchKernelGGL((qkv_finish_kernel<128, true>), g2, blk, 0, st, b);
-      else hipLaunchKernelGGL((qkv_finish_kernel<128, false>), g2, blk, 0, st, b);
+      if (kv8) hipLaunchKernelGGL((qkv_finish_kernel<128, true>), g2, blk2, 0, st, b);
+      else hipLaunchKernelGGL((qkv_finish_kernel<128, false>), g2, blk2, 0, st, b);
     } else {
       return hipErrorInvalidValue;
     }
