@@ -434,6 +434,49 @@ __global__ void __launch_bounds__(256) qkv_partial_kernel(QKVArgs a) {
   }
 }
 
+// Stores pairs (d + i, d + D/2 + i), i < 4, of one (token, head): q to
+// q_out, k / v to their cache slot (slots outside the pool are skipped); 4
+// dims per store where rows are 4-element aligned (checked on the host).
+template <int D, bool KV8>
+__device__ __forceinline__ void store_pairs(const QKVArgs& a, int kind, int h, int64_t tok, int d, const float (&x1)[4],
+                                            const float (&x2)[4]) {
+  constexpr int PPH = D / 2;
+  auto put_bf16 = [&](uint16_t* p, const float (&x)[4]) {
+    if (a.vec_stores) {
+      st8(p, u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])});
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = (uint16_t)pack_bf16x2(x[i], 0.f);
+    }
+  };
+  if (kind == 0) {
+    if (!a.q_out) return;
+    uint16_t* op = (uint16_t*)a.q_out + tok * a.q_out_row_stride + (int64_t)h * D + d;
+    put_bf16(op, x1);
+    put_bf16(op + PPH, x2);
+    return;
+  }
+  const int64_t slot = a.slot_mapping[tok];
+  if (slot < 0 || slot >= a.num_slots) return;
+  char* cp = (char*)(kind == 1 ? a.k_cache : a.v_cache) + (slot * a.cache_slot_stride + (int64_t)h * D + d) * (KV8 ? 1 : 2);
+  if (KV8) {
+    const uint32_t w1 = pack_fp8x4(x1[0], x1[1], x1[2], x1[3]), w2 = pack_fp8x4(x2[0], x2[1], x2[2], x2[3]);
+    if (a.vec_stores) {
+      *reinterpret_cast<uint32_t*>(cp) = w1;
+      *reinterpret_cast<uint32_t*>(cp + PPH) = w2;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        cp[i] = (char)(w1 >> (8 * i));
+        cp[PPH + i] = (char)(w2 >> (8 * i));
+      }
+    }
+  } else {
+    put_bf16(reinterpret_cast<uint16_t*>(cp), x1);
+    put_bf16(reinterpret_cast<uint16_t*>(cp) + PPH, x2);
+  }
+}
+
 // One thread per 4 rotation pairs (d .. d+3, d+D/2 .. d+D/2+3) of one
 // (token, head): 16-byte partial loads, and 4 values per store (8 bytes bf16,
 // 4 bytes fp8).
@@ -472,40 +515,150 @@ __global__ void __launch_bounds__(64) qkv_finish_kernel(QKVArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) rope_pair_bf16(x1[i], x2[i], bf16_bits_to_f32(cp[i]), bf16_bits_to_f32(sp[i]));
   }
-  // 4 values per store where rows are 4-element aligned (checked on the host)
-  auto put_bf16 = [&](uint16_t* p, const float (&x)[4]) {
-    if (a.vec_stores) {
-      st8(p, u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])});
-    } else {
+  store_pairs<D, KV8>(a, kind, h, tok, d, x1, x2);
+}
+
+// Few tokens (decode): one 8-wave workgroup per (head, 8 CB rotation pairs)
+// -- output columns 8 CB c .. 8 CB (c+1) - 1 and the same plus D/2 of one
+// head -- over the whole hidden dimension, for up to 16 TB tokens (blockIdx.y:
+// the next 16 TB).  Wave w takes K range [w K/8, (w+1) K/8): all of its weight
+// operands are loaded at once (one memory round trip; the weights are the
+// bytes that matter, MK bounds the k-steps and so the registers), x operands
+// (L2-resident) a k-step ahead, on v_mfma_f32_16x16x32_bf16 (A = x rows,
+// B = W^T, 16 columns = 8 pairs per block).  The 8 partial sums meet in LDS
+// and are added in wave order (deterministic), rounded like F.linear,
+// rotated and stored 4 dims at a time.  No partials in HBM, no second launch.
+template <int D, bool KV8, int MK, int CB, int TB>
+__global__ void __launch_bounds__(512) qkv_small_kernel(QKVArgs a) {
+  constexpr int NWV = 8;
+  constexpr int NC = 16 * CB;             // output columns per workgroup
+  constexpr int TM = 16 * TB;             // tokens per workgroup
+  __shared__ __attribute__((aligned(16))) float red[NWV][TM][NC + 1];   // [wave][token][column]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  constexpr int GPH = D / NC;             // column groups per head
+  const int head = blockIdx.x / GPH, cg = blockIdx.x % GPH;
+  const int kind = head < a.num_q_heads ? 0 : (head < a.num_q_heads + a.num_kv_heads ? 1 : 2);
+  const int h = kind == 0 ? head : (kind == 1 ? head - a.num_q_heads : head - a.num_q_heads - a.num_kv_heads);
+  const char* w = (const char*)(kind == 0 ? a.w_q : (kind == 1 ? a.w_k : a.w_v));
+  const int64_t wstride = kind == 0 ? a.w_q_row_stride : (kind == 1 ? a.w_k_row_stride : a.w_v_row_stride);
+  const int64_t N = a.num_tokens;
+  const int64_t tok0 = (int64_t)blockIdx.y * TM;
+  const int ntb = (int)min<int64_t>(TB, (N - tok0 + 15) / 16);   // 16-token blocks present
+  const int kq = 8 * (lane >> 4);
+  const int ksteps = a.hidden / (NWV * 32);
+  const int kw0 = wave * ksteps * 32;
+  u32x4 wb[CB][MK];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) p[i] = (uint16_t)pack_bf16x2(x[i], 0.f);
-    }
-  };
-  if (kind == 0) {
-    uint16_t* op = (uint16_t*)a.q_out + tok * a.q_out_row_stride + (int64_t)h * D + d;
-    put_bf16(op, x1);
-    put_bf16(op + PPH, x2);
-    return;
+  for (int cb = 0; cb < CB; ++cb) {
+    // lane's B column: pair lane & 7 of the block, first (lane & 8 == 0) or second half of the head
+    const int col = (lane & 8 ? D / 2 : 0) + 8 * (CB * cg + cb) + (lane & 7);
+    const char* wrow = w + ((int64_t)h * D + col) * wstride * 2 + (int64_t)(kw0 + kq) * 2;
+#pragma unroll
+    for (int s = 0; s < MK; ++s)
+      if (s < ksteps) wb[cb][s] = ld16(wrow + s * 64);
   }
-  const int64_t slot = a.slot_mapping[tok];
-  if (slot < 0 || slot >= a.num_slots) return;
-  char* cp = (char*)(kind == 1 ? a.k_cache : a.v_cache) + (slot * a.cache_slot_stride + (int64_t)h * D + d) * (KV8 ? 1 : 2);
-  if (KV8) {
-    const uint32_t w1 = pack_fp8x4(x1[0], x1[1], x1[2], x1[3]), w2 = pack_fp8x4(x2[0], x2[1], x2[2], x2[3]);
-    if (a.vec_stores) {
-      *reinterpret_cast<uint32_t*>(cp) = w1;
-      *reinterpret_cast<uint32_t*>(cp + PPH) = w2;
-    } else {
+  f32x4 acc[CB][TB];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        cp[i] = (char)(w1 >> (8 * i));
-        cp[PPH + i] = (char)(w2 >> (8 * i));
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int t = 0; t < TB; ++t) acc[cb][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const char* xrow[TB];
+#pragma unroll
+  for (int t = 0; t < TB; ++t) {
+    const int64_t tk = min(tok0 + 16 * t + (lane & 15), N - 1);
+    xrow[t] = (const char*)a.x + tk * a.x_row_stride * 2 + (int64_t)(kw0 + kq) * 2;
+  }
+  // x operands PF k-steps ahead (statically indexed: only PF + 1 steps' registers live)
+  constexpr int PF = MK <= 8 ? MK : 2;
+  u32x4 xa[MK][TB];
+#pragma unroll
+  for (int s = 0; s < PF; ++s)
+#pragma unroll
+    for (int t = 0; t < TB; ++t)
+      if (s < ksteps && t < ntb) xa[s][t] = ld16(xrow[t] + s * 64);
+#pragma unroll
+  for (int s = 0; s < MK; ++s) {
+    if (s < ksteps) {
+      if (s + PF < MK && s + PF < ksteps) {
+#pragma unroll
+        for (int t = 0; t < TB; ++t)
+          if (t < ntb) xa[s + PF][t] = ld16(xrow[t] + (s + PF) * 64);
       }
+#pragma unroll
+      for (int t = 0; t < TB; ++t)
+        if (t < ntb) {
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb)
+            acc[cb][t] = mfma16(__builtin_bit_cast(bf16x8, xa[s][t]), __builtin_bit_cast(bf16x8, wb[cb][s]),
+                                acc[cb][t]);
+        }
     }
-  } else {
-    put_bf16(reinterpret_cast<uint16_t*>(cp), x1);
-    put_bf16(reinterpret_cast<uint16_t*>(cp) + PPH, x2);
   }
+  // lane holds partial D[token 16t + 4(lane >> 4) + j][column 16cb + (lane & 15)]
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int t = 0; t < TB; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) red[wave][16 * t + 4 * (lane >> 4) + j][16 * cb + (lane & 15)] = acc[cb][t][j];
+  __syncthreads();
+  // thread: one token, 4 pairs (pairs 4q .. 4q+3 of column block q / 2)
+  if (tid >= TM * 2 * CB) return;
+  const int tr = tid / (2 * CB), q = tid % (2 * CB);
+  const int64_t tok = tok0 + tr;
+  if (tok >= N) return;
+  const int c1 = 16 * (q >> 1) + 4 * (q & 1);   // red column of the first half's first pair
+  float x1[4], x2[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int v = 0; v < NWV; ++v) {       // fixed wave order: deterministic sums
+      s1 += red[v][tr][c1 + i];
+      s2 += red[v][tr][c1 + 8 + i];
+    }
+    x1[i] = s1;
+    x2[i] = s2;
+    round2_bf16(x1[i], x2[i]);            // F.linear's bf16 output
+  }
+  // padded rows of the [B, T_q] layout: nothing written, cos/sin not read
+  if (a.query_lens && tok % a.tokens_per_seq >= a.query_lens[tok / a.tokens_per_seq]) return;
+  const int d = 8 * (CB * cg + (q >> 1)) + 4 * (q & 1);   // first head dim of the thread's 4 pairs
+  if (kind == 1 || (kind == 0 && a.rotate_q)) {
+    const int64_t crow = a.rope_rows ? a.rope_rows[tok] : tok;
+    const uint16_t* cp = (const uint16_t*)a.cos + crow * a.rope_row_stride + d;
+    const uint16_t* sp = (const uint16_t*)a.sin + crow * a.rope_row_stride + d;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rope_pair_bf16(x1[i], x2[i], bf16_bits_to_f32(cp[i]), bf16_bits_to_f32(sp[i]));
+  }
+  store_pairs<D, KV8>(a, kind, h, tok, d, x1, x2);
+}
+
+template <int D, bool KV8, int CB>
+static void launch_qkv_small(const QKVArgs& b, int heads, hipStream_t st) {
+  constexpr int TB = 2;
+  const dim3 grid((unsigned)(heads * (D / (16 * CB))), (unsigned)((b.num_tokens + 16 * TB - 1) / (16 * TB))), block(512);
+  const int ks = b.hidden / 256;
+  if (ks <= 8) hipLaunchKernelGGL((qkv_small_kernel<D, KV8, 8, CB, TB>), grid, block, 0, st, b);
+  else hipLaunchKernelGGL((qkv_small_kernel<D, KV8, 16, CB, TB>), grid, block, 0, st, b);
+}
+
+#ifndef QKV_SMALL_MAX_TOKENS
+#define QKV_SMALL_MAX_TOKENS 32
+#endif
+// Single-launch path for few tokens: column blocks per wave (1 or 2) such
+// that the workgroups (one per 16 CB columns) fit on the CUs at once, or 0
+// when the batch takes another path.  Up to 16 k-steps per wave (hidden
+// <= 4096): beyond that the weight registers of a workgroup take more than
+// one memory round trip and the split-K path is faster.
+static int qkv_small_cb(int64_t n, int hidden, int heads, int head_dim, int cus) {
+  if (n <= 0 || n > QKV_SMALL_MAX_TOKENS || hidden % 256 != 0 || hidden > 4096 || (head_dim != 64 && head_dim != 128))
+    return 0;
+  const int64_t cols = (int64_t)heads * head_dim;
+  if (cols / 16 <= cus) return 1;
+  if (cols / 32 <= cus) return 2;
+  return 0;
 }
 
 // Split-K plan for a batch: chunk length (multiple of 32, >= 256) and count,
@@ -525,6 +678,7 @@ static void qkv_split_plan(int64_t n, int hidden, int heads, int cus, int* chunk
 }
 
 size_t qkv_workspace_bytes(int64_t n, int hidden, int heads, int head_dim, int cus) {
+  if (qkv_small_cb(n, hidden, heads, head_dim, cus)) return 0;
   int chunk, count;
   qkv_split_plan(n, hidden, heads, cus, &chunk, &count);
   return count > 1 ? (size_t)count * n * heads * head_dim * sizeof(float) : 0;
@@ -544,6 +698,17 @@ hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t st) {
   b.vec_stores = al8(a.k_cache) && al8(a.v_cache) && a.cache_slot_stride % 4 == 0 &&
                  (!a.q_out || (al8(a.q_out) && a.q_out_row_stride % 4 == 0));
   const bool kv8 = a.kv_dtype == kFP8;
+  // few tokens: one launch, whole K per workgroup
+  if (const int cb = qkv_small_cb(a.num_tokens, a.hidden, heads, a.head_dim, a.cus)) {
+    if (a.head_dim == 64) {
+      if (cb == 1) kv8 ? launch_qkv_small<64, true, 1>(b, heads, st) : launch_qkv_small<64, false, 1>(b, heads, st);
+      else kv8 ? launch_qkv_small<64, true, 2>(b, heads, st) : launch_qkv_small<64, false, 2>(b, heads, st);
+    } else {
+      if (cb == 1) kv8 ? launch_qkv_small<128, true, 1>(b, heads, st) : launch_qkv_small<128, false, 1>(b, heads, st);
+      else kv8 ? launch_qkv_small<128, true, 2>(b, heads, st) : launch_qkv_small<128, false, 2>(b, heads, st);
+    }
+    return hipGetLastError();
+  }
   int chunk, count;
   qkv_split_plan(a.num_tokens, a.hidden, heads, a.cus, &chunk, &count);
   if (count > 1 && a.workspace &&

@@ -151,7 +151,7 @@ def test_qkv_rejects_bad_arguments():
         paged.qkv_rope_kv_write(x32, None, w32, w32, cs.float(), cs.float(), kc.float(), kc.float().clone(), sl)
 
 
-@pytest.mark.parametrize("n,hidden,Hq,Hkv,D", [(64, 2048, 32, 8, 64), (70, 1024, 8, 2, 128), (3, 4096, 32, 8, 128)])
+@pytest.mark.parametrize("n,hidden,Hq,Hkv,D", [(64, 2048, 32, 8, 64), (70, 1024, 8, 2, 128), (100, 4096, 32, 8, 128)])
 def test_qkv_split_k_exact_and_matches_tile_path(n, hidden, Hq, Hkv, D):
     """Few tokens: the hidden dimension is split over workgroups (fp32
     partials summed in fixed order by a second launch).  Sparse small
@@ -207,6 +207,67 @@ def test_qkv_split_k_random_matches_tile_path():
     _close_bf16(res[0][0], res[1][0], "q", True)
     _close_bf16(res[0][1], res[1][1], "k", True)
     _close_bf16(res[0][2], res[1][2], "v", False)
+
+
+# (n, hidden, Hq, Hkv, D, kv dtype, rotate_q, with q): 1B / 8B head shapes
+# (16-column and 32-column workgroups), a ragged second 16-token block, fp8
+# cache, unrotated q, no q heads
+SMALL_CASES = [(1, 2048, 32, 8, 64, BF, True, True), (32, 2048, 32, 8, 64, torch.float8_e4m3fn, True, True),
+               (17, 4096, 32, 8, 128, BF, True, True), (9, 4096, 32, 8, 128, torch.float8_e4m3fn, False, True),
+               (30, 768, 4, 4, 64, BF, True, False), (5, 256, 2, 1, 128, BF, False, True)]
+
+
+@pytest.mark.parametrize("n,hidden,Hq,Hkv,D,kvd,rotate_q,with_q", SMALL_CASES)
+def test_qkv_few_tokens_single_launch(n, hidden, Hq, Hkv, D, kvd, rotate_q, with_q):
+    """Up to 32 tokens with hidden a multiple of 256 (<= 4096): one launch,
+    each workgroup the whole hidden dimension of 16 or 32 output columns
+    (eight waves split K and add their partials in LDS), so no workspace is
+    planned.  Small-integer data: bit-exact against the oracle."""
+    print(f"qkv few tokens n={n} hidden={hidden} Hq={Hq} Hkv={Hkv} D={D} kv={kvd} rot={rotate_q} q={with_q}",
+          flush=True)
+    from gllm_amd import _lib
+    assert _lib.load().gllm_qkv_workspace_bytes(n, hidden, Hq, Hkv, D, int(with_q)) == 0
+    q, qr, kc, vc, kr, vr, slots, ns = _run(n, hidden, Hq, Hkv, D, True, 50 + n, kv_dtype=kvd, rotate_q=rotate_q,
+                                            with_q=with_q)
+    if with_q:
+        assert torch.equal(q.cpu().view(torch.int16), qr.view(torch.int16))
+    else:
+        assert q is None
+    iv = torch.uint8 if kvd != BF else torch.int16
+    assert torch.equal(kc.view(iv), kr.view(iv))
+    assert torch.equal(vc.view(iv), vr.view(iv))
+
+
+@pytest.mark.parametrize("n,hidden,Hq,Hkv,D", [(16, 4096, 32, 8, 128), (32, 2048, 32, 8, 64)])
+def test_qkv_few_tokens_random_data(n, hidden, Hq, Hkv, D):
+    """The single-launch path on N(0,1) data at the 8B / 1B shapes: within
+    the GEMM's accumulation-order rounding of the oracle."""
+    print(f"qkv few tokens random n={n} hidden={hidden} D={D}", flush=True)
+    q, qr, kc, vc, kr, vr, slots, ns = _run(n, hidden, Hq, Hkv, D, False, 60 + n)
+    _close_bf16(q, qr, "q", True)
+    _close_bf16(kc[slots], kr[slots], "k", True)
+    _close_bf16(vc[slots], vr[slots], "v", False)
+
+
+def test_qkv_few_tokens_padded_rows():
+    """Padded rows of a [B, T_q] layout on the single-launch path: skipped,
+    their slots keep the sentinel."""
+    print("qkv few tokens, padded rows", flush=True)
+    B, Tq, hidden, Hq, Hkv, D = 4, 8, 512, 4, 2, 128
+    n = B * Tq
+    x, (wq, wk, wv), cos_t, sin_t, pos, slots, ns = _inputs(n, hidden, Hq, Hkv, D, True, 71)
+    ql = torch.tensor([8, 3, 1, 5], dtype=torch.int32)
+    kc = torch.full((ns, Hkv, D), 3.0, dtype=BF)
+    vc = kc.clone()
+    kg, vg = kc.to(DEV), vc.to(DEV)
+    q = paged.qkv_rope_kv_write(x.to(DEV), wq.to(DEV), wk.to(DEV), wv.to(DEV), cos_t.to(DEV), sin_t.to(DEV), kg, vg,
+                                slots.to(DEV), query_lens=ql.to(DEV), rope_rows=pos.to(DEV))
+    torch.cuda.synchronize()
+    real = (torch.arange(n) % Tq) < ql.repeat_interleave(Tq)
+    qr = op.qkv_rope_kv_write(x, wq, wk, wv, cos_t[pos], sin_t[pos], kc, vc, slots, Hkv, D, real=real)
+    assert torch.equal(kg.cpu().view(torch.int16), kc.view(torch.int16))
+    assert torch.equal(vg.cpu().view(torch.int16), vc.view(torch.int16))
+    assert torch.equal(q.cpu()[real].view(torch.int16), qr[real].view(torch.int16))
 
 
 @pytest.mark.parametrize("integer,rotate_q", [(True, True), (False, True), (True, False)])

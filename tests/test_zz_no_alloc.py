@@ -48,7 +48,7 @@ def _call(lib, noalloc, x, w, cos, sin, pos, slots, ns, Hq, Hkv, D, ws=None):
 def test_noalloc_matches_workspace_entry_point(hidden, Hq, Hkv, D):
     print(f"qkv noalloc hidden={hidden} D={D}", flush=True)
     lib = _lib.load()
-    for n, seed in ((64, 1), (24, 2)):            # second call smaller: stale partials must not leak
+    for n, seed in ((64, 1), (40, 2)):            # second call smaller: stale partials must not leak
         inp = _inputs(n, hidden, Hq, Hkv, D, seed)
         need = lib.gllm_qkv_workspace_bytes(n, hidden, Hq, Hkv, D, 1)
         assert need > 0                           # the split-K path (the one with scratch) runs
