@@ -494,11 +494,21 @@ __global__ void __launch_bounds__(64) qkv_finish_kernel(QKVArgs a) {
   const int h = kind == 0 ? head : (kind == 1 ? head - a.num_q_heads : head - a.num_q_heads - a.num_kv_heads);
   const int64_t F = (int64_t)heads * D;
   const float* ws = a.workspace + tok * F + (int64_t)head * D + d;
+  // every chunk's loads in flight at once (the plan makes at most 16 chunks)
+  f32x4 p1[16], p2[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c)
+    if (c < a.split_count) {
+      p1[c] = *reinterpret_cast<const f32x4*>(ws + (int64_t)c * a.num_tokens * F);
+      p2[c] = *reinterpret_cast<const f32x4*>(ws + (int64_t)c * a.num_tokens * F + PPH);
+    }
   f32x4 s1 = {0.f, 0.f, 0.f, 0.f}, s2 = {0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < a.split_count; ++c) {   // chunk order fixed: deterministic sums
-    s1 += *reinterpret_cast<const f32x4*>(ws + (int64_t)c * a.num_tokens * F);
-    s2 += *reinterpret_cast<const f32x4*>(ws + (int64_t)c * a.num_tokens * F + PPH);
-  }
+#pragma unroll
+  for (int c = 0; c < 16; ++c)
+    if (c < a.split_count) {                    // chunk order fixed: deterministic sums
+      s1 += p1[c];
+      s2 += p2[c];
+    }
   float x1[4], x2[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
