@@ -466,6 +466,9 @@ def main():
     ap.add_argument("--no-ceilings", action="store_true", help="skip the copy / GEMM reference measurements")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a plain 256 MiB device copy (known bytes) for counter calibration")
+    ap.add_argument("--qkv-sweep", action="store_true",
+                    help="only time the QKV projection path over token counts at the 1B / 8B / 70B layer shapes "
+                         "(one JSON line) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: --gpus must be 1 (how the path would "
@@ -473,6 +476,17 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.qkv_sweep:
+        rows = []
+        for name, hid, hq, hkv, hd in (("1B", 2048, 32, 8, 64), ("8B", 4096, 32, 8, 128), ("70B", 8192, 64, 8, 128)):
+            for n in (1, 16, 32, 64, 128, 256, 512, 1024, 2048):
+                r = bench_qkv(n, hid, hq, hkv, hd, 24 if n <= 256 else 4, args.warmup, 15, dev)
+                rows.append({"layer": name, **{k: r[k] for k in ("tokens", "fused_ms", "dispatched_ms", "unfused_ms",
+                                                                 "hbm_frac", "mfma_frac")}})
+                progress(f"qkv {name} n={n}: fused {r['fused_ms'] * 1e3:.1f} us, dispatched "
+                         f"{r['dispatched_ms'] * 1e3:.1f} us, unfused {r['unfused_ms'] * 1e3:.1f} us")
+        print(json.dumps({"qkv_sweep": rows}))
+        return
     cfgs = args.configs.split(",")
     reps = max(args.steps, 1)
     cpu = not args.no_cpu
@@ -496,6 +510,9 @@ def main():
         r, _, _ = bench_paged(dd, 1, args.warmup, reps, 4, dev, args.split, args.hw, eager=False)
         r["roofline"] = roofline_hbm(r["bytes_per_launch"], r["ms_per_step"], "decode_8b")
         extra["decode_8b"] = r
+        torch.cuda.empty_cache()
+        # fused QKV projection + RoPE + KV write for (d)'s 256 decode tokens (8B layer)
+        extra["qkv_decode_8b"] = bench_qkv(256, 4096, 32, 8, 128, 8, args.warmup, max(10, reps // 3), dev)
         torch.cuda.empty_cache()
     if "c" in cfgs:
         progress("config (c)")
@@ -533,6 +550,8 @@ def main():
         torch.cuda.empty_cache()
         # fused QKV projection + RoPE + KV write for the same 64 decode tokens (1B layer)
         extra["qkv_decode_1b"] = bench_qkv(64, 2048, 32, 8, 64, 24, args.warmup, max(10, reps // 3), dev)
+        # 16 decode tokens: the single-launch path (up to 32 tokens)
+        extra["qkv_decode_1b_16"] = bench_qkv(16, 2048, 32, 8, 64, 24, args.warmup, max(10, reps // 3), dev)
         torch.cuda.empty_cache()
     if "a" in cfgs:
         progress("config (a)")
