@@ -13,16 +13,18 @@
 // Tiling: one 4-wave workgroup per (128 tokens, one head of D outputs); for
 // large batches at D = 128, one 8-wave workgroup per (256 tokens, two heads)
 // whose waves each take 64 tokens x one head (two row blocks share every W
-// operand read), launched in XCD-grouped order (qkv_groups).  X and W
+// operand read); both launched in XCD-grouped order (qkv_groups).  X and W
 // K-slices of 32 stream HBM/L2 -> LDS with global_load_lds into a 4-stage
 // ring (XOR-swizzled 16-byte chunks: operand reads are bank-conflict free);
 // each wave computes 32 tokens x D outputs per row block on
 // v_mfma_f32_32x32x16_bf16 (D/32 accumulator blocks).  Output column n of
 // block b is head dim 32b + n, so a RoPE pair (d, d + D/2) sits in blocks b
 // and b + D/64 of the same lane: the rotation happens in registers and every
-// value is stored from its lane (2-byte stores, 64-byte runs per half-wave).  Batches too
-// small to fill the GPU with such tiles split the hidden dimension
-// (qkv_partial_kernel + qkv_finish_kernel, below).
+// value is stored from its lane (4 dims per store where rows are aligned).
+// Batches too small to fill the GPU with such tiles split the hidden
+// dimension (qkv_partial_kernel + qkv_finish_kernel, below); up to 32 tokens
+// take one launch with the whole hidden dimension per workgroup
+// (qkv_small_kernel).
 #include <algorithm>
 
 #include "common.h"
@@ -47,7 +49,7 @@ __host__ __device__ inline QKVGroups qkv_groups(int64_t tiles, int ngroups, int 
     if (c <= slots && ngroups % c == 0) { gh = c; break; }
   QKVGroups g;
   g.gh = gh;
-  g.gt = slots / gh > 0 ? slots / gh : 1;
+  g.gt = (int)std::max<int64_t>(1, std::min<int64_t>(tiles, slots / gh));
   g.nhg = (ngroups + gh - 1) / gh;
   g.nsg = ((tiles + g.gt - 1) / g.gt) * g.nhg;
   return g;
@@ -357,15 +359,33 @@ __global__ void __launch_bounds__(256) qkv_partial_kernel(QKVArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[NS * STAGE];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int head = blockIdx.y;
+  // 1-D grid over token tiles x (chunk, head) groups, in XCD-grouped order
+  // when there are several token tiles: the tiles of a group run on one XCD,
+  // so its W slice comes from HBM once and its other reads hit that XCD's L2
+  const int heads = a.num_q_heads + 2 * a.num_kv_heads;
+  const int ngroups = heads * a.split_count;
+  const int64_t N = a.num_tokens;
+  int tile, gi;
+  if (N <= TM) {
+    tile = 0;
+    gi = blockIdx.x;
+  } else {
+    const QKVGroups gr = qkv_groups((N + TM - 1) / TM, ngroups, a.cus);
+    const int S = gr.gt * gr.gh;
+    const int b = blockIdx.x, xcd = b % kXcds, j = b / kXcds;
+    const int sg = xcd + kXcds * (j / S), wi = j % S;
+    tile = (sg / gr.nhg) * gr.gt + wi / gr.gh;
+    gi = (sg % gr.nhg) * gr.gh + wi % gr.gh;
+    if ((int64_t)tile * TM >= N || gi >= ngroups) return;   // padding of the last super-groups
+  }
+  const int head = gi % heads, chunk = gi / heads;
   const int kind = head < a.num_q_heads ? 0 : (head < a.num_q_heads + a.num_kv_heads ? 1 : 2);
   const int h = kind == 0 ? head : (kind == 1 ? head - a.num_q_heads : head - a.num_q_heads - a.num_kv_heads);
   const char* w = (const char*)(kind == 0 ? a.w_q : (kind == 1 ? a.w_k : a.w_v));
   const int64_t wstride = kind == 0 ? a.w_q_row_stride : (kind == 1 ? a.w_k_row_stride : a.w_v_row_stride);
   w += (int64_t)h * D * wstride * 2;
-  const int64_t N = a.num_tokens;
-  const int64_t tok0 = (int64_t)blockIdx.x * TM;
-  const int kc0 = blockIdx.z * a.split_chunk;
+  const int64_t tok0 = (int64_t)tile * TM;
+  const int kc0 = chunk * a.split_chunk;
   const int nk = min(a.split_chunk, a.hidden - kc0) / BK;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
 
@@ -424,7 +444,7 @@ __global__ void __launch_bounds__(256) qkv_partial_kernel(QKVArgs a) {
   }
   if (!wact) return;
   const int64_t F = (int64_t)(a.num_q_heads + 2 * a.num_kv_heads) * D;
-  float* ws = a.workspace + (int64_t)blockIdx.z * N * F + (int64_t)head * D + fh * (D / 2) + (lane & 31);
+  float* ws = a.workspace + (int64_t)chunk * N * F + (int64_t)head * D + fh * (D / 2) + (lane & 31);
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     const int64_t tok = tok0 + tb * 32 + 8 * (j / 4) + 4 * hi + (j % 4);
@@ -725,7 +745,11 @@ hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t st) {
       a.workspace_bytes >= (size_t)count * a.num_tokens * heads * a.head_dim * sizeof(float)) {
     b.split_chunk = chunk;
     b.split_count = count;
-    const dim3 g1((unsigned)((a.num_tokens + 63) / 64), (unsigned)heads, (unsigned)count), blk(256);
+    const QKVGroups gr1 = qkv_groups((a.num_tokens + 63) / 64, heads * count, a.cus);
+    const int64_t wgs1 = a.num_tokens <= 64 ? (int64_t)heads * count
+                                            : (int64_t)kXcds * gr1.gt * gr1.gh * ((gr1.nsg + kXcds - 1) / kXcds);
+    if (wgs1 > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 g1((unsigned)wgs1), blk(256);
     const int hpb = 64 / (a.head_dim / 8);    // heads per finish workgroup (one wave)
     const dim3 g2((unsigned)a.num_tokens, (unsigned)((heads + hpb - 1) / hpb)), blk2(64);
     if (a.head_dim == 64) {
@@ -741,26 +765,31 @@ hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t st) {
     }
     return hipGetLastError();
   }
-  const dim3 grid((unsigned)tiles, (unsigned)heads), block(256);
+  // 128-token tiles, one head each, in XCD-grouped order (a head's token
+  // tiles share its W slice through one XCD's L2)
+  const QKVGroups gr = qkv_groups(tiles, heads, a.cus);
+  const int64_t wgs = (int64_t)kXcds * gr.gt * gr.gh * ((gr.nsg + kXcds - 1) / kXcds);
+  if (wgs > 0x7fffffff) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)wgs), block(256);
   if (a.head_dim == 64) {
-    if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<64, true, 128>), grid, block, 0, st, b);
-    else hipLaunchKernelGGL((qkv_rope_write_kernel<64, false, 128>), grid, block, 0, st, b);
+    if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<64, true, 128, 1, 1, true>), grid, block, 0, st, b);
+    else hipLaunchKernelGGL((qkv_rope_write_kernel<64, false, 128, 1, 1, true>), grid, block, 0, st, b);
   } else if (a.head_dim == 128) {
     // Large batches: 256 tokens x 2 heads per 8-wave workgroup (each wave 64
     // tokens x one head: two row blocks share every W operand read), in
     // XCD-grouped order; they need heads that pair within q and within k/v.
     const int64_t tiles2 = (a.num_tokens + 255) / 256;
     if (b.num_q_heads % 2 == 0 && a.num_kv_heads % 2 == 0 && tiles2 * (heads / 2) >= 2 * (int64_t)a.cus) {
-      const QKVGroups gr = qkv_groups(tiles2, heads / 2, a.cus);
-      const int64_t wgs = (int64_t)kXcds * gr.gt * gr.gh * ((gr.nsg + kXcds - 1) / kXcds);
-      if (wgs > 0x7fffffff) return hipErrorInvalidValue;
-      const dim3 grid2((unsigned)wgs), block2(512);
+      const QKVGroups gr2 = qkv_groups(tiles2, heads / 2, a.cus);
+      const int64_t wgs2 = (int64_t)kXcds * gr2.gt * gr2.gh * ((gr2.nsg + kXcds - 1) / kXcds);
+      if (wgs2 > 0x7fffffff) return hipErrorInvalidValue;
+      const dim3 grid2((unsigned)wgs2), block2(512);
       if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<128, true, 256, 2, 2, true>), grid2, block2, 0, st, b);
       else hipLaunchKernelGGL((qkv_rope_write_kernel<128, false, 256, 2, 2, true>), grid2, block2, 0, st, b);
       return hipGetLastError();
     }
-    if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<128, true, 128>), grid, block, 0, st, b);
-    else hipLaunchKernelGGL((qkv_rope_write_kernel<128, false, 128>), grid, block, 0, st, b);
+    if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<128, true, 128, 1, 1, true>), grid, block, 0, st, b);
+    else hipLaunchKernelGGL((qkv_rope_write_kernel<128, false, 128, 1, 1, true>), grid, block, 0, st, b);
   } else {
     return hipErrorInvalidValue;
   }
