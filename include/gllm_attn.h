@@ -117,13 +117,16 @@ int gllm_qkv_rope_kv_write(const void* x, int64_t x_row_stride, int64_t num_toke
                            int32_t head_dim, int32_t dtype, int32_t kv_dtype, void* workspace,
                            size_t workspace_bytes, void* stream);
 /* Device bytes gllm_qkv_rope_kv_write can use as `workspace` for this batch
- * (0: none).  With a workspace of at least that size, batches too small to
- * fill the GPU with (128-token x head) tiles (decode) split the hidden
- * dimension over more workgroups: fp32 partial sums go to the workspace and
- * a second small launch sums them in fixed order (deterministic) before the
- * RoPE and the stores.  Without it the tile kernel runs (same results up to
- * the fp32 summation order of the projections).  No library counterpart in
- * the reference: F.linear needs none. */
+ * (0: none).  Up to 32 tokens (hidden a multiple of 256, at most 4096) the
+ * projection runs in one launch with no workspace (each workgroup the whole
+ * hidden dimension of 16 or 32 output columns).  Otherwise, with a
+ * workspace of at least that size, batches too small to fill the GPU with
+ * (128-token x head) tiles (decode) split the hidden dimension over more
+ * workgroups: fp32 partial sums go to the workspace and a second small
+ * launch sums them in fixed order (deterministic) before the RoPE and the
+ * stores.  Without it the tile kernel runs (same results up to the fp32
+ * summation order of the projections).  No library counterpart in the
+ * reference: F.linear needs none. */
 size_t gllm_qkv_workspace_bytes(int64_t num_tokens, int32_t hidden, int32_t num_q_heads, int32_t num_kv_heads,
                                 int32_t head_dim, int32_t with_q);
 
