@@ -169,7 +169,11 @@ qkv_rope_write_kernel(QKVArgs a) {
       wait_vmcnt<0>();
     __syncthreads();                           // stage ks visible; stage ks - 1 free
     if (ks + NS - 1 < nk) dma(ks + NS - 1, (ks + NS - 1) % NS);
-    if (wact) {
+    // Every wave multiplies, also one whose rows are all past the batch (it
+    // reads the clamped copies of the last row and stores nothing): a branch
+    // here makes the compiler move the accumulators between AGPRs and VGPRs
+    // on every k-step.
+    {
       const char* As = lds + (ks % NS) * STAGE;
       const char* Bs = As + A_BYTES;
 #pragma unroll
@@ -426,7 +430,7 @@ __global__ void __launch_bounds__(256) qkv_partial_kernel(QKVArgs a) {
     wait_stages<IPS, NS - 2>(min(NS - 2, nk - 1 - ks));   // stage ks in; later stages may still fly
     __syncthreads();
     if (ks + NS - 1 < nk) dma(ks + NS - 1, (ks + NS - 1) % NS);
-    if (wact) {
+    {   // every wave multiplies (no branch: accumulators stay in place), inactive ones store nothing
       const char* As = lds + (ks % NS) * STAGE;
       const char* Bs = As + A_BYTES;
 #pragma unroll
