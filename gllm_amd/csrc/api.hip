@@ -1,6 +1,7 @@
 // C ABI of libgllm_attn: argument validation, the host work planner and the
 // kernel launches.  Declarations and contracts: include/gllm_attn.h.
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cmath>
 #include <cstdio>
@@ -71,13 +72,27 @@ void block_div(int32_t bs, uint32_t* magic, int32_t* shift) {
 constexpr int32_t kMaxBlockSize = 65536;
 
 // Compute units of the current device (256 when there is none, e.g. a CPU-only host).
+// CUs of the current device (256 when there is none), queried once per
+// device: plans and projection calls ask on every engine step.
 int device_cus() {
+  constexpr int kDevs = 64;
+  static std::atomic<int> known[kDevs] = {};
   int dev = 0;
-  hipDeviceProp_t prop;
-  if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0)
-    return prop.multiProcessorCount;
-  (void)hipGetLastError();
-  return 256;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  if (dev < kDevs) {
+    const int c = known[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  if (dev < kDevs) known[dev].store(n, std::memory_order_relaxed);
+  return n;
 }
 
 // Pinned staging buffers of plans, reused across plans (an engine builds one
@@ -524,13 +539,7 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
   }
 
   if (mfma) {
-    int cus = 256;
-    int dev = 0;
-    hipDeviceProp_t prop;
-    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0)
-      cus = prop.multiProcessorCount;
-    else
-      (void)hipGetLastError();
+    const int cus = device_cus();
     int64_t n_pf = 0;
     for (int i = 0; i < num_seqs; ++i)
       if ((int64_t)query_lens[i] * G > 16) ++n_pf;
