@@ -346,20 +346,23 @@ __device__ __forceinline__ void wait_stages(int after) {
   }
 }
 
-template <int D>
+template <int D, int BK, int NS>
 __global__ void __launch_bounds__(256) qkv_partial_kernel(QKVArgs a) {
   constexpr int TM = 64;                  // tokens per workgroup (waves: 2 token blocks x 2 output halves)
-  constexpr int BK = 32;
-  constexpr int NS = 4;
   constexpr int NBW = D / 64;             // 32 x 32 blocks per wave (D/2 outputs)
   constexpr int ROWB = BK * 2;
-  constexpr int A_BYTES = TM * ROWB;      // 4 KB
+  constexpr int CPR = BK / 8;             // 16-byte chunks per LDS row
+  constexpr int A_BYTES = TM * ROWB;
   constexpr int B_BYTES = D * ROWB;
   constexpr int STAGE = A_BYTES + B_BYTES;
   constexpr int IA = A_BYTES / (256 * 16);
   constexpr int IB = B_BYTES / (256 * 16);
   constexpr int IPS = IA + IB;
-  static_assert(IA == 1 && IB >= 1, "tile / workgroup mismatch");
+  static_assert(IA >= 1 && IB >= 1 && (CPR == 4 || CPR == 8), "tile / workgroup mismatch");
+  // physical chunk of logical chunk c in row r: 64-byte rows as the tile
+  // kernel; 128-byte rows XOR with r & 7 (8 consecutive rows, one logical
+  // chunk: 8 distinct 4-bank groups)
+  auto swz = [](int r) { return CPR == 4 ? qkv_swz(r) : (r & 7); };
   __shared__ __attribute__((aligned(16))) char lds[NS * STAGE];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -399,7 +402,7 @@ __global__ void __launch_bounds__(256) qkv_partial_kernel(QKVArgs a) {
     for (int i = 0; i < IPS; ++i) {
       const bool isA = i < IA;
       const int c = (isA ? i : i - IA) * 256 + tid;
-      const int row = c >> 2, lc = (c & 3) ^ qkv_swz(row);
+      const int row = c / CPR, lc = (c % CPR) ^ swz(row);
       const char* src;
       if (isA) {
         const int64_t t = min(tok0 + row, N - 1);
@@ -436,11 +439,11 @@ __global__ void __launch_bounds__(256) qkv_partial_kernel(QKVArgs a) {
 #pragma unroll
       for (int kk = 0; kk < BK / 16; ++kk) {
         const int lc = 2 * kk + hi;
-        const bf16x8 av = __builtin_bit_cast(bf16x8, ld16(As + ar * ROWB + ((lc ^ qkv_swz(ar)) << 4)));
+        const bf16x8 av = __builtin_bit_cast(bf16x8, ld16(As + ar * ROWB + ((lc ^ swz(ar)) << 4)));
 #pragma unroll
         for (int b = 0; b < NBW; ++b) {
           const int br = fh * (D / 2) + 32 * b + (lane & 31);
-          const bf16x8 bv = __builtin_bit_cast(bf16x8, ld16(Bs + br * ROWB + ((lc ^ qkv_swz(br)) << 4)));
+          const bf16x8 bv = __builtin_bit_cast(bf16x8, ld16(Bs + br * ROWB + ((lc ^ swz(br)) << 4)));
           acc[b] = mfma32(av, bv, acc[b]);
         }
       }
@@ -695,6 +698,13 @@ static int qkv_small_cb(int64_t n, int hidden, int heads, int head_dim, int cus)
   return 0;
 }
 
+// Split-K partials: K steps of 64 (each X / W row slice is one whole
+// 128-byte line, half the memory requests per byte of 32-wide steps) and a
+// 2-stage LDS ring (48 KB at D = 128: three workgroups per CU).  Measured
+// against 32-wide steps in a 4-stage ring: 8B layer 64 / 256 / 512 tokens
+// 23.5 / 44.9 / 61.0 -> 20.9 / 39.9 / 51.2 us; 3 and 4 stages were slower.
+constexpr int kQkvPartialBK = 64, kQkvPartialNS = 2;
+
 // Split-K plan for a batch: chunk length (multiple of 32, >= 256) and count,
 // or count 1 when the tile kernel already has enough workgroups.
 static void qkv_split_plan(int64_t n, int hidden, int heads, int cus, int* chunk, int* count) {
@@ -706,7 +716,8 @@ static void qkv_split_plan(int64_t n, int hidden, int heads, int cus, int* chunk
   int64_t want = (2 * (int64_t)cus + wgs64 - 1) / wgs64;           // about two workgroups per CU
   want = std::min<int64_t>(std::min<int64_t>(want, hidden / 256), 16);   // the finish kernel sums <= 16 chunks
   if (want <= 1) return;
-  const int c = (int)(((hidden + want - 1) / want + 31) / 32 * 32);
+  const int g = hidden % kQkvPartialBK == 0 ? kQkvPartialBK : 32;   // chunks in whole k-steps of the partial kernel
+  const int c = (int)(((hidden + want - 1) / want + g - 1) / g * g);
   *chunk = c;
   *count = (hidden + c - 1) / c;
 }
@@ -756,12 +767,15 @@ hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t st) {
     const dim3 g1((unsigned)wgs1), blk(256);
     const int hpb = 64 / (a.head_dim / 8);    // heads per finish workgroup (one wave)
     const dim3 g2((unsigned)a.num_tokens, (unsigned)((heads + hpb - 1) / hpb)), blk2(64);
+    const bool bk64 = kQkvPartialBK == 64 && a.hidden % 64 == 0;
     if (a.head_dim == 64) {
-      hipLaunchKernelGGL((qkv_partial_kernel<64>), g1, blk, 0, st, b);
+      if (bk64) hipLaunchKernelGGL((qkv_partial_kernel<64, 64, kQkvPartialNS>), g1, blk, 0, st, b);
+      else hipLaunchKernelGGL((qkv_partial_kernel<64, 32, 4>), g1, blk, 0, st, b);
       if (kv8) hipLaunchKernelGGL((qkv_finish_kernel<64, true>), g2, blk2, 0, st, b);
       else hipLaunchKernelGGL((qkv_finish_kernel<64, false>), g2, blk2, 0, st, b);
     } else if (a.head_dim == 128) {
-      hipLaunchKernelGGL((qkv_partial_kernel<128>), g1, blk, 0, st, b);
+      if (bk64) hipLaunchKernelGGL((qkv_partial_kernel<128, 64, kQkvPartialNS>), g1, blk, 0, st, b);
+      else hipLaunchKernelGGL((qkv_partial_kernel<128, 32, 4>), g1, blk, 0, st, b);
       if (kv8) hipLaunchKernelGGL((qkv_finish_kernel<128, true>), g2, blk2, 0, st, b);
       else hipLaunchKernelGGL((qkv_finish_kernel<128, false>), g2, blk2, 0, st, b);
     } else {

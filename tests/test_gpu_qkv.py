@@ -151,7 +151,9 @@ def test_qkv_rejects_bad_arguments():
         paged.qkv_rope_kv_write(x32, None, w32, w32, cs.float(), cs.float(), kc.float(), kc.float().clone(), sl)
 
 
-@pytest.mark.parametrize("n,hidden,Hq,Hkv,D", [(64, 2048, 32, 8, 64), (70, 1024, 8, 2, 128), (100, 4096, 32, 8, 128)])
+# hidden 544 (not a multiple of 64): the partial kernel's 32-wide K steps
+@pytest.mark.parametrize("n,hidden,Hq,Hkv,D", [(64, 2048, 32, 8, 64), (70, 1024, 8, 2, 128), (100, 4096, 32, 8, 128),
+                                               (40, 544, 4, 2, 64)])
 def test_qkv_split_k_exact_and_matches_tile_path(n, hidden, Hq, Hkv, D):
     """Few tokens: the hidden dimension is split over workgroups (fp32
     partials summed in fixed order by a second launch).  Sparse small
