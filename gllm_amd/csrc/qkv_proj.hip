@@ -70,17 +70,34 @@ __device__ __forceinline__ int qkv_swz(int r) { return (r >> 2) & 3; }
 
 }  // namespace
 
+// s_waitcnt vmcnt(after * IPS) for a run-time `after` in [0, M].
+template <int IPS, int M>
+__device__ __forceinline__ void wait_stages(int after) {
+  if constexpr (M >= 0) {
+    if (after >= M) {
+      wait_vmcnt<M * IPS>();
+      return;
+    }
+    wait_stages<IPS, M - 1>(after);
+  }
+}
+
 // TM tokens x HP heads per workgroup; each wave computes 32 RB tokens x one
-// head (RB row blocks share every W operand read).
-template <int D, bool KV8, int TM, int RB = 1, int HP = 1, bool GROUPED = false>
+// head (RB row blocks share every W operand read).  K slices of BK per
+// stage of an NS-stage LDS ring.
+template <int D, bool KV8, int TM, int RB = 1, int HP = 1, bool GROUPED = false, int BK = 32, int NS = 4>
 __global__ void __launch_bounds__(64 * (TM / (32 * RB)) * HP) __attribute__((amdgpu_waves_per_eu(2)))
 qkv_rope_write_kernel(QKVArgs a) {
   constexpr int TG = TM / (32 * RB);      // token groups (waves per head)
   constexpr int NT = 64 * TG * HP;        // threads
-  constexpr int BK = 32;                  // K slice per stage
-  constexpr int NS = 4;                   // LDS ring stages
   constexpr int NB = D / 32;              // accumulator blocks per row block (32 x 32 each)
-  constexpr int ROWB = BK * 2;            // 64-byte LDS rows
+  constexpr int ROWB = BK * 2;            // LDS row: one K slice of a token / W row
+  constexpr int CPR = BK / 8;             // 16-byte chunks per LDS row
+  static_assert(CPR == 4 || CPR == 8, "K slice of 32 or 64");
+  // physical chunk of logical chunk c in row r: 64-byte rows rotate by
+  // qkv_swz, 128-byte rows XOR with r & 7 (8 consecutive rows reading one
+  // logical chunk hit 8 distinct 4-bank groups)
+  auto swz = [](int r) { return CPR == 4 ? qkv_swz(r) : (r & 7); };
   constexpr int A_BYTES = TM * ROWB;      // X slice
   constexpr int B_BYTES = HP * D * ROWB;  // W slice (HP heads of one kind, consecutive W rows)
   constexpr int STAGE = A_BYTES + B_BYTES;
@@ -119,16 +136,16 @@ qkv_rope_write_kernel(QKVArgs a) {
   const int nk = a.hidden / BK;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
 
-  // Copy instruction i of this thread: 16-byte chunk c = i * 256 + tid of the
-  // stage's X (i < IA) or W part; LDS row c / 4, physical chunk c % 4, which
-  // holds logical chunk (c % 4) ^ qkv_swz(row).
+  // Copy instruction i of this thread: 16-byte chunk c = i * NT + tid of the
+  // stage's X (i < IA) or W part; LDS row c / CPR, physical chunk c % CPR,
+  // which holds logical chunk (c % CPR) ^ swz(row).
   auto dma = [&](int ks, int stage) {
     const int64_t k0b = (int64_t)ks * BK * 2;
 #pragma unroll
     for (int i = 0; i < IPS; ++i) {
       const bool isA = i < IA;
       const int c = (isA ? i : i - IA) * NT + tid;
-      const int row = c >> 2, lc = (c & 3) ^ qkv_swz(row);
+      const int row = c / CPR, lc = (c % CPR) ^ swz(row);
       const char* src;
       if (isA) {
         const int64_t t = min(tok0 + row, N - 1);     // rows past the batch re-read the last token
@@ -160,13 +177,7 @@ qkv_rope_write_kernel(QKVArgs a) {
   for (int ks = 0; ks < nk; ++ks) {
     // this thread's copies of stage ks are done once at most the copies of the
     // (up to NS - 2) later stages already issued are outstanding
-    const int after = min(NS - 2, nk - 1 - ks);
-    if (after >= 2)
-      wait_vmcnt<2 * IPS>();
-    else if (after == 1)
-      wait_vmcnt<IPS>();
-    else
-      wait_vmcnt<0>();
+    wait_stages<IPS, NS - 2>(min(NS - 2, nk - 1 - ks));
     __syncthreads();                           // stage ks visible; stage ks - 1 free
     if (ks + NS - 1 < nk) dma(ks + NS - 1, (ks + NS - 1) % NS);
     // Every wave multiplies, also one whose rows are all past the batch (it
@@ -183,12 +194,12 @@ qkv_rope_write_kernel(QKVArgs a) {
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
           const int arr = ar + 32 * r;
-          av[r] = __builtin_bit_cast(bf16x8, ld16(As + arr * ROWB + ((lc ^ qkv_swz(arr)) << 4)));
+          av[r] = __builtin_bit_cast(bf16x8, ld16(As + arr * ROWB + ((lc ^ swz(arr)) << 4)));
         }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
           const int br = bh + 32 * b + (lane & 31);
-          const bf16x8 bv = __builtin_bit_cast(bf16x8, ld16(Bs + br * ROWB + ((lc ^ qkv_swz(br)) << 4)));
+          const bf16x8 bv = __builtin_bit_cast(bf16x8, ld16(Bs + br * ROWB + ((lc ^ swz(br)) << 4)));
 #pragma unroll
           for (int r = 0; r < RB; ++r) acc[r][b] = mfma32(av[r], bv, acc[r][b]);
         }
@@ -334,18 +345,6 @@ qkv_rope_write_kernel(QKVArgs a) {
 // [chunk][token][head * D + d]); qkv_finish_kernel sums the chunks in fixed
 // order (deterministic), rounds like F.linear and does the RoPE and the
 // stores exactly as the tile kernel's epilogue.
-// s_waitcnt vmcnt(after * IPS) for a run-time `after` in [0, M].
-template <int IPS, int M>
-__device__ __forceinline__ void wait_stages(int after) {
-  if constexpr (M >= 0) {
-    if (after >= M) {
-      wait_vmcnt<M * IPS>();
-      return;
-    }
-    wait_stages<IPS, M - 1>(after);
-  }
-}
-
 template <int D, int BK, int NS>
 __global__ void __launch_bounds__(256) qkv_partial_kernel(QKVArgs a) {
   constexpr int TM = 64;                  // tokens per workgroup (waves: 2 token blocks x 2 output halves)
@@ -681,16 +680,14 @@ static void launch_qkv_small(const QKVArgs& b, int heads, hipStream_t st) {
   else hipLaunchKernelGGL((qkv_small_kernel<D, KV8, 16, CB, TB>), grid, block, 0, st, b);
 }
 
-#ifndef QKV_SMALL_MAX_TOKENS
-#define QKV_SMALL_MAX_TOKENS 32
-#endif
+constexpr int64_t kQkvSmallMaxTokens = 32;   // beyond: split-K is faster (x re-read per 16 columns)
 // Single-launch path for few tokens: column blocks per wave (1 or 2) such
 // that the workgroups (one per 16 CB columns) fit on the CUs at once, or 0
 // when the batch takes another path.  Up to 16 k-steps per wave (hidden
 // <= 4096): beyond that the weight registers of a workgroup take more than
 // one memory round trip and the split-K path is faster.
 static int qkv_small_cb(int64_t n, int hidden, int heads, int head_dim, int cus) {
-  if (n <= 0 || n > QKV_SMALL_MAX_TOKENS || hidden % 256 != 0 || hidden > 4096 || (head_dim != 64 && head_dim != 128))
+  if (n <= 0 || n > kQkvSmallMaxTokens || hidden % 256 != 0 || hidden > 4096 || (head_dim != 64 && head_dim != 128))
     return 0;
   const int64_t cols = (int64_t)heads * head_dim;
   if (cols / 16 <= cus) return 1;
@@ -728,6 +725,15 @@ size_t qkv_workspace_bytes(int64_t n, int hidden, int heads, int head_dim, int c
   qkv_split_plan(n, hidden, heads, cus, &chunk, &count);
   return count > 1 ? (size_t)count * n * heads * head_dim * sizeof(float) : 0;
 }
+
+// Tile kernels take K slices of 64 in a 2-stage ring when hidden allows:
+// whole 128-byte lines per row slice (half the memory requests per byte of
+// 32-wide slices).  Measured against 32-wide slices in a 4-stage ring:
+// 1B layer 1,024 / 4,096 tokens 41.5 / 109.3 -> 33.4 / 90.6 us, 8B
+// 1,024 / 4,096 / 19,679 tokens 90.4 / 274 / 1,247 -> 82.2 / 246 / 1,223 us;
+// 3 stages (one workgroup per CU) were slower.
+constexpr bool kTileBK64 = true, kTileBig64 = true;
+constexpr int kTileNS = 2;
 
 hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t st) {
   if (a.num_tokens == 0) return hipSuccess;
@@ -789,9 +795,15 @@ hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t st) {
   const int64_t wgs = (int64_t)kXcds * gr.gt * gr.gh * ((gr.nsg + kXcds - 1) / kXcds);
   if (wgs > 0x7fffffff) return hipErrorInvalidValue;
   const dim3 grid((unsigned)wgs), block(256);
+  const bool bk64 = kTileBK64 && a.hidden % 64 == 0;
   if (a.head_dim == 64) {
-    if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<64, true, 128, 1, 1, true>), grid, block, 0, st, b);
-    else hipLaunchKernelGGL((qkv_rope_write_kernel<64, false, 128, 1, 1, true>), grid, block, 0, st, b);
+    if (bk64) {
+      if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<64, true, 128, 1, 1, true, 64, kTileNS>), grid, block, 0, st, b);
+      else hipLaunchKernelGGL((qkv_rope_write_kernel<64, false, 128, 1, 1, true, 64, kTileNS>), grid, block, 0, st, b);
+    } else {
+      if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<64, true, 128, 1, 1, true>), grid, block, 0, st, b);
+      else hipLaunchKernelGGL((qkv_rope_write_kernel<64, false, 128, 1, 1, true>), grid, block, 0, st, b);
+    }
   } else if (a.head_dim == 128) {
     // Large batches: 256 tokens x 2 heads per 8-wave workgroup (each wave 64
     // tokens x one head: two row blocks share every W operand read), in
@@ -802,12 +814,22 @@ hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t st) {
       const int64_t wgs2 = (int64_t)kXcds * gr2.gt * gr2.gh * ((gr2.nsg + kXcds - 1) / kXcds);
       if (wgs2 > 0x7fffffff) return hipErrorInvalidValue;
       const dim3 grid2((unsigned)wgs2), block2(512);
-      if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<128, true, 256, 2, 2, true>), grid2, block2, 0, st, b);
-      else hipLaunchKernelGGL((qkv_rope_write_kernel<128, false, 256, 2, 2, true>), grid2, block2, 0, st, b);
+      if (bk64 && kTileBig64) {
+        if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<128, true, 256, 2, 2, true, 64, 2>), grid2, block2, 0, st, b);
+        else hipLaunchKernelGGL((qkv_rope_write_kernel<128, false, 256, 2, 2, true, 64, 2>), grid2, block2, 0, st, b);
+      } else {
+        if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<128, true, 256, 2, 2, true>), grid2, block2, 0, st, b);
+        else hipLaunchKernelGGL((qkv_rope_write_kernel<128, false, 256, 2, 2, true>), grid2, block2, 0, st, b);
+      }
       return hipGetLastError();
     }
-    if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<128, true, 128, 1, 1, true>), grid, block, 0, st, b);
-    else hipLaunchKernelGGL((qkv_rope_write_kernel<128, false, 128, 1, 1, true>), grid, block, 0, st, b);
+    if (bk64) {
+      if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<128, true, 128, 1, 1, true, 64, kTileNS>), grid, block, 0, st, b);
+      else hipLaunchKernelGGL((qkv_rope_write_kernel<128, false, 128, 1, 1, true, 64, kTileNS>), grid, block, 0, st, b);
+    } else {
+      if (kv8) hipLaunchKernelGGL((qkv_rope_write_kernel<128, true, 128, 1, 1, true>), grid, block, 0, st, b);
+      else hipLaunchKernelGGL((qkv_rope_write_kernel<128, false, 128, 1, 1, true>), grid, block, 0, st, b);
+    }
   } else {
     return hipErrorInvalidValue;
   }

@@ -92,9 +92,9 @@ def rope_kv_write(k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torc
 
 # Token count from which qkv_rope_kv_write projects with hipBLASLt (three
 # F.linear calls) and then runs the RoPE + KV write kernel: on MI355X the
-# fused kernel is ahead up to ~1k tokens (3.6x at 64 tokens, 1.03x at 1024)
-# and behind from ~2k (0.90x at 2048, 0.80x at 19679 tokens, 8B shapes).
-QKV_UNFUSED_FROM = 1536
+# fused kernel is ahead up to ~2k tokens (8B shapes: 4.3x at 64 tokens, 1.1x
+# at 2048) and behind from ~4k (0.90x at 4096, 0.82x at 19679 tokens).
+QKV_UNFUSED_FROM = 3072
 
 
 def qkv_rope_kv_write(x: torch.Tensor, w_q: torch.Tensor | None, w_k: torch.Tensor, w_v: torch.Tensor,
