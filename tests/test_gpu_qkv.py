@@ -272,6 +272,38 @@ def test_qkv_few_tokens_padded_rows():
     assert torch.equal(q.cpu()[real].view(torch.int16), qr[real].view(torch.int16))
 
 
+def _random_shapes(count, seed):
+    """Seeded shapes over all three fused paths: up to 32 tokens (single
+    launch), split-K (64- and 32-wide K steps) and the tile kernels."""
+    import random
+    r = random.Random(seed)
+    out = []
+    for _ in range(count):
+        D = r.choice([64, 128])
+        Hkv = r.choice([1, 2, 4])
+        Hq = Hkv * r.choice([1, 2, 4])
+        hidden = r.choice([32 * r.randint(8, 64), 256 * r.randint(1, 8)])   # 256 .. 2048; multiples of 32 / 256
+        n = r.choice([r.randint(1, 32), r.randint(33, 160), r.randint(161, 700)])
+        kvd = r.choice([BF, torch.float8_e4m3fn])
+        out.append((n, hidden, Hq, Hkv, D, kvd, r.random() < 0.8, r.random() < 0.85))
+    return out
+
+
+@pytest.mark.parametrize("n,hidden,Hq,Hkv,D,kvd,rotate_q,with_q", _random_shapes(16, 2024))
+def test_qkv_random_shapes_exact(n, hidden, Hq, Hkv, D, kvd, rotate_q, with_q):
+    """Random shapes (seeded), small-integer data: every fused path is
+    bit-exact against the oracle."""
+    print(f"qkv random shape n={n} hidden={hidden} Hq={Hq} Hkv={Hkv} D={D} kv={kvd} rot={rotate_q} q={with_q}",
+          flush=True)
+    q, qr, kc, vc, kr, vr, slots, ns = _run(n, hidden, Hq, Hkv, D, True, 90 + n, kv_dtype=kvd, rotate_q=rotate_q,
+                                            with_q=with_q)
+    if with_q:
+        assert torch.equal(q.cpu().view(torch.int16), qr.view(torch.int16))
+    iv = torch.uint8 if kvd != BF else torch.int16
+    assert torch.equal(kc.view(iv), kr.view(iv))
+    assert torch.equal(vc.view(iv), vr.view(iv))
+
+
 @pytest.mark.parametrize("integer,rotate_q", [(True, True), (False, True), (True, False)])
 def test_qkv_large_batch_unfused_route(integer, rotate_q):
     """From paged.QKV_UNFUSED_FROM tokens the projections go through F.linear
