@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs d,c,b,a,e]
 
-Prints ONE JSON line.  The headline (``value``) is BASELINE config (d), the
+Prints ONE JSON line.  The headline (``value``) is benchmark config (d), the
 metric's 8B GQA shape: one paged-attention launch over a mixed continuous
 batch (256 decode sequences + 4 chunked prefills of 512 tokens, Llama-3.1-8B
 heads), in GB/s of compulsory HBM bytes per launch, inputs resident in HBM.
@@ -471,8 +471,8 @@ def main():
                          "(one JSON line) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only: --gpus must be 1 (how the path would "
-                                   "shard over several GPUs is described in DESIGN.md; nothing multi-GPU is built)"}))
+        print(json.dumps({"error": "this build runs on one GPU only: --gpus must be 1 (nothing multi-GPU is "
+                                   "built; the path would shard by sequence or kv head with no exchange)"}))
         sys.exit(2)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)

@@ -1,5 +1,5 @@
 // Generic attention: paged decode/prefill and the dense-bias op for fp32
-// models (BASELINE config (a)) and for bf16 models whose head dim the MFMA
+// models (benchmark config (a)) and for bf16 models whose head dim the MFMA
 // kernels do not take (not 64 or 128; up to 256).  One wave per (query head,
 // query row, sequence), 64 keys per step, exact online softmax (expf) in
 // fp32.  Compiled with -ffp-contract=off so the q rotation rounds each op

@@ -1,4 +1,4 @@
-"""Seeded synthetic inputs for the BASELINE configurations.
+"""Seeded synthetic inputs for the benchmark configurations.
 
 Conventions: CPU ``torch.Generator`` seeds 0 (lengths), 1 (block tables) and
 2 (values); values are N(0, 1) drawn in fp32 and cast to the model dtype;

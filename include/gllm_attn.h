@@ -3,7 +3,7 @@
  *
  * Drop-in boundary for the attention path of TheEpicDolphin/gllm.  The
  * reference is pure Python and binds no FFI; these entry points are what its
- * call sites would bind (through ctypes):
+ * call sites would bind (through ctypes; gllm_amd/_lib.py is such a binding):
  *
  *   gllm_rope_kv_write    replaces gllm/model/layers/attention.py:151-161
  *                         (Attention.apply_rope :76-119 on k [and q], then the

@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 
-Used for BASELINE config (a): a random-init Llama-3.2-1B-shaped model run
+Used for benchmark config (a): a random-init Llama-3.2-1B-shaped model run
 through the reference's batching path, recording per-layer attention outputs
 and the greedy tokens.  Follows:
 

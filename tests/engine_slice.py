@@ -1,4 +1,4 @@
-"""GPU engine slice for BASELINE config (a): the Llama-shaped model of
+"""GPU engine slice for benchmark config (a): the Llama-shaped model of
 ``oracle.engine`` run on the GPU, with the attention hot path on the product
 (``gllm_amd.Attention`` + ``PagedKVCache``) and plain torch for the
 projections, norms, MLP and logits (outside the hot path).

@@ -7,7 +7,7 @@ import torch
 from gllm_amd import workloads
 from oracle import attention as oa
 
-MAX_ABS = 2e-2   # bf16 output vs fp32 reference, BASELINE tolerance
+MAX_ABS = 2e-2   # bf16 output vs fp32 reference, the benchmark tolerance
 MEAN_ABS = 2e-3
 
 

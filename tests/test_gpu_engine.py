@@ -1,4 +1,4 @@
-"""BASELINE config (a): a random-init Llama-3.2-1B-shaped model (16 layers,
+"""benchmark config (a): a random-init Llama-3.2-1B-shaped model (16 layers,
 hidden 2048, 32/8 heads, head_dim 64, FFN 8192, vocab 128256, RoPE theta
 5e5, fp32 weights from seed 3) through the reference's batching path: 8
 prompts of uniform-random ids (lengths U{8..64}, seed 4), greedy decode of

@@ -1,4 +1,4 @@
-"""GPU parity at the BASELINE configurations' full sizes.
+"""GPU parity at the benchmark configurations' full sizes.
 
 Where the CPU oracle would take too long on every row, rows are sampled: a
 query row r of sequence i is checked as its own one-row "sequence" with

@@ -280,7 +280,7 @@ def test_lse_split_merge_identity():
     assert torch.allclose(oa.lse_merge(ms, ls, accs), full, atol=1e-6)
 
 
-# ------------------------------------------------------------ fused projection
+# ------------------------------------------------------------ fused projection (attention.py:139-161)
 def test_oracle_linear_brute_force():
     """linear.py:13-19 (F.linear: x @ W^T, W [out, in]) on tiny inputs against
     Python-float dot products, rounded once to bf16."""
