@@ -118,3 +118,54 @@ def test_whole_decode_step_graph(dtype):
         for li in range(L):
             assert torch.equal(bits(outs[li]), bits(eager[li])), f"replay {rep} layer {li}"
         assert torch.equal(cache.physical_kv_cache.view(torch.uint8), cache_after.view(torch.uint8))
+
+
+@pytest.mark.parametrize("n", [16, 64, 700])
+def test_qkv_projection_graph(n):
+    """The fused QKV projection + RoPE + KV write (attention.py:139-161)
+    captured in a HIP graph on each of its paths (16 tokens: one launch; 64:
+    split-K partials + finish, with the cached workspace; 700: tile kernel):
+    every replay, with eager work between, equals the eager call bit for bit
+    in q and in the written cache."""
+    from oracle import rope as orope
+    print(f"qkv graph n={n}", flush=True)
+    g = torch.Generator().manual_seed(200 + n)
+    hidden, Hq, Hkv, D = 2048, 32, 8, 64
+    bf = torch.bfloat16
+    x = torch.randn(n, hidden, generator=g).to(bf).cuda()
+    w = [(torch.randn(h * D, hidden, generator=g) / hidden ** 0.5).to(bf).cuda() for h in (Hq, Hkv, Hkv)]
+    cos_t, sin_t = orope.rope_cache(4096, D, 500000.0, bf)
+    cos_t, sin_t = cos_t.cuda(), sin_t.cuda()
+    pos = torch.randint(0, 4096, (n,), generator=g).cuda()
+    ns = 2 * n + 16
+    slots = torch.randperm(ns, generator=g)[:n].cuda()
+    kc = torch.zeros(ns, Hkv, D, dtype=bf, device="cuda")
+    vc = torch.zeros_like(kc)
+    q_out = torch.empty(n, Hq, D, dtype=bf, device="cuda")
+
+    def call():
+        paged.qkv_rope_kv_write(x, w[0], w[1], w[2], cos_t, sin_t, kc, vc, slots, q_out=q_out, rope_rows=pos,
+                                unfused_from=None)
+
+    call()
+    torch.cuda.synchronize()
+    q_eager, k_eager, v_eager = q_out.clone(), kc.clone(), vc.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for rep in range(4):
+        q_out.fill_(float("nan"))                       # eager work between replays
+        kc.zero_()
+        vc.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(q_out.view(torch.int16), q_eager.view(torch.int16)), f"q replay {rep}"
+        assert torch.equal(kc.view(torch.int16), k_eager.view(torch.int16)), f"k replay {rep}"
+        assert torch.equal(vc.view(torch.int16), v_eager.view(torch.int16)), f"v replay {rep}"
