@@ -588,9 +588,13 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
       if (fills) {
         best_S = cap;
       } else {
+        // about half as many items as resident slots, at least 256 keys each:
+        // a split's partial write and merge cost more than the parallelism
+        // of smaller ones buys (measured: 2 x 8000-key 8B sequences 48.8 ->
+        // 38.7 us, config (a)'s 16-layer bf16 decode step 229 -> 194 us)
         const int64_t hg = (num_kv_heads + best_hw - 1) / best_hw;
-        best_S = (decode_tokens * hg + target - 1) / std::max<int64_t>(target, 1);
-        best_S = std::max<int64_t>((best_S + 31) / 32 * 32, 128);
+        best_S = (2 * decode_tokens * hg + target - 1) / std::max<int64_t>(target, 1);
+        best_S = std::max<int64_t>((best_S + 31) / 32 * 32, 256);
       }
     }
     best_S = std::min(best_S, cap);
@@ -609,12 +613,18 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
       const int L = s.ctx_len + s.q_len;
       if (s.q_len * G <= 16) {
         ++p->n_decode_seqs;
+        // equal splits of 16-key multiples (a remainder split after full
+        // S-key ones was the slowest item): len = ceil16(ceil(L / n)) for
+        // the final n, which the kernel recomputes from (L, nsplits) alone
         s.nsplits = (int32_t)((L + S - 1) / S);
+        int64_t len = split_len_of(L, s.nsplits);
+        s.nsplits = (int32_t)((L + len - 1) / len);
+        len = split_len_of(L, s.nsplits);
         s.partial_base = (int32_t)p->n_partials;
         if (s.nsplits > 1) p->n_partials += (int64_t)num_kv_heads * s.nsplits;
         for (int sp = 0; sp < s.nsplits; ++sp)
           for (int hg = 0; hg < hgroups; ++hg) {
-            const int64_t keys = std::min<int64_t>(L, (int64_t)(sp + 1) * S) - (int64_t)sp * S;
+            const int64_t keys = std::min<int64_t>(L, (int64_t)(sp + 1) * len) - (int64_t)sp * len;
             dc.push_back({keys, WorkItem{kItemDecode | (hg << 8), i, sp, s.q_row_start, s.ctx_len, s.q_len,
                                          s.nsplits, s.partial_base}});
           }

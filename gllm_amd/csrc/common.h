@@ -210,6 +210,13 @@ struct SeqInfo {
 
 enum : int32_t { kItemPrefill = 0, kItemDecode = 1 };
 
+// Keys per split of a decode sequence of L keys cut into n equal splits
+// (16-key multiples; the last split takes the rest).  The planner picks n so
+// that every split is non-empty: n = ceil(L / split_len_of(L, n0)).
+__host__ __device__ inline int32_t split_len_of(int64_t L, int32_t n) {
+  return (int32_t)(((L + n - 1) / n + 15) / 16 * 16);
+}
+
 // One workgroup's work, with its sequence's facts folded in so the kernel's
 // prologue needs one dependent load less.
 struct WorkItem {

@@ -451,15 +451,18 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
     st8(op + 16 * d, u32x2{pack_bf16x2(ox[d][0] * inv, ox[d][1] * inv), pack_bf16x2(ox[d][2] * inv, ox[d][3] * inv)});
 }
 
-// One decode work item of the split-launch planner (fixed split_len; split
-// partials merged by merge_splits_kernel).
+// One decode work item of the split-launch planner (split it.a of the
+// sequence's it.nsplits equal key ranges; split partials merged by
+// merge_splits_kernel).
 template <int D, int HW, int KW, bool KV8>
 __device__ __forceinline__ void decode_wg(const AttnArgs& a, const WorkItem& it, char* lds) {
   DecodeTask tk;
   tk.seq = it.seq;
   tk.hg = it.kind_b >> 8;
-  tk.kbeg = it.a * a.split_len;
-  tk.kend = min(it.ctx_len + it.q_len, tk.kbeg + a.split_len);
+  const int L = it.ctx_len + it.q_len;
+  const int len = split_len_of(L, it.nsplits);   // equal splits (the planner's split_len bounds them)
+  tk.kbeg = it.a * len;
+  tk.kend = min(L, tk.kbeg + len);
   tk.q_row_start = it.q_row_start;
   tk.ctx_len = it.ctx_len;
   tk.q_len = it.q_len;
