@@ -71,9 +71,8 @@ void block_div(int32_t bs, uint32_t* magic, int32_t* shift) {
 }
 constexpr int32_t kMaxBlockSize = 65536;
 
-// Compute units of the current device (256 when there is none, e.g. a CPU-only host).
-// CUs of the current device (256 when there is none), queried once per
-// device: plans and projection calls ask on every engine step.
+// CUs of the current device (256 when there is none, e.g. a CPU-only host),
+// queried once per device: plans and projection calls ask on every engine step.
 int device_cus() {
   constexpr int kDevs = 64;
   static std::atomic<int> known[kDevs] = {};
@@ -209,6 +208,8 @@ struct BalancedShape {
   int hw, hgroups;
   int64_t units, wgs;
 };
+// Decode-path sequences (q_len x G <= 16 query rows) only: in a mixed batch
+// the others are prefill items.
 BalancedShape balanced_shape(const gllm_attn_plan* p, int cus, int heads_req) {
   BalancedShape b{};
   b.hw = heads_req;
@@ -217,7 +218,9 @@ BalancedShape balanced_shape(const gllm_attn_plan* p, int cus, int heads_req) {
     while (b.hw > 1 && p->Hkv % b.hw) b.hw /= 2;
   }
   b.hgroups = (p->Hkv + b.hw - 1) / b.hw;
-  for (const SeqInfo& si : p->seqs) b.units += (int64_t)b.hgroups * ((si.ctx_len + si.q_len + 15) / 16);
+  const int G = p->Hq / p->Hkv;
+  for (const SeqInfo& si : p->seqs)
+    if (si.q_len * G <= 16) b.units += (int64_t)b.hgroups * ((si.ctx_len + si.q_len + 15) / 16);
   b.wgs = std::max<int64_t>(1, std::min<int64_t>(b.units, (int64_t)cus * GLLM_DECODE_WG_PER_CU(p->D)));
   return b;
 }
@@ -232,24 +235,30 @@ BalancedShape balanced_shape(const gllm_attn_plan* p, int cus, int heads_req) {
 // 740-770; the cut sits between the measured points.
 int64_t balanced_min_units_per_wg(int D) { return D == 128 ? 192 : 128; }
 
-void plan_balanced_decode(gllm_attn_plan* p, int cus, int heads_req) {
+// wgs > 0: that many workgroups (a mixed launch's decode share), else one
+// per resident decode slot.
+void plan_balanced_decode(gllm_attn_plan* p, int cus, int heads_req, int64_t wgs) {
   const BalancedShape shape = balanced_shape(p, cus, heads_req);
   const int hw = shape.hw, hgroups = shape.hgroups;
   const int64_t bs = p->bs;
+  const int G = p->Hq / p->Hkv;
   // a segment's keys start on a 16-key unit, so a block size that is not a
   // power of two <= 16 can add one partial block at the front: stay <= 511
   const int64_t ucap = std::max<int64_t>(1, (is_pow2(bs) && bs <= 16 ? 512 * bs : 510 * bs) / 16);
-  const int64_t U = shape.units, W = shape.wgs;
+  const int64_t U = shape.units;
+  const int64_t W = wgs > 0 ? std::max<int64_t>(1, std::min(wgs, U)) : shape.wgs;
   p->heads_per_wg = hw;
   p->decode_waves = 8;
   p->split_len = 0;
-  p->n_decode_seqs = p->num_seqs;
+  p->n_decode_seqs = 0;
   p->segs.clear();
   p->seg_ptr.assign((size_t)W + 1, 0);
   std::vector<int32_t> seg_wg;
   int64_t u0 = 0, j = 0;
   for (int i = 0; i < p->num_seqs; ++i) {
     SeqInfo& si = p->seqs[i];
+    if (si.q_len * G > 16) continue;   // a prefill item of the mixed launch
+    ++p->n_decode_seqs;
     si.nsplits = 1;
     const int L = si.ctx_len + si.q_len;
     const int64_t nu = (L + 15) / 16;
@@ -280,6 +289,108 @@ void plan_balanced_decode(gllm_attn_plan* p, int cus, int heads_req) {
   }
   for (int32_t w : seg_wg) ++p->seg_ptr[(size_t)w + 1];
   for (int64_t w = 0; w < W; ++w) p->seg_ptr[(size_t)w + 1] += p->seg_ptr[(size_t)w];
+}
+
+// A prefill work item: 8 waves over the (query head, 32-row block) pairs
+// c = w*8 .. w*8+7 of one kv head (row block c / G, head c % G), with its
+// last visible key + 1 and its (query row, visible key) pairs.
+struct PrefillPiece {
+  WorkItem it;
+  int64_t kend;
+  int64_t pairs;
+};
+void prefill_pieces(const SeqInfo& s, int i, int G, int Hkv, std::vector<PrefillPiece>& out) {
+  constexpr int pw = 8;
+  const int nrb = (s.q_len + 31) / 32;
+  const int nwg = (G * nrb + pw - 1) / pw;
+  for (int h = 0; h < Hkv; ++h)
+    for (int w = 0; w < nwg; ++w) {
+      const int c0 = w * pw, c1 = std::min(w * pw + pw - 1, G * nrb - 1);
+      const int64_t kend = s.ctx_len + std::min(s.q_len - 1, (c1 / G) * 32 + 31) + 1;
+      int64_t pairs = 0;
+      for (int c = c0; c <= c1; ++c) {
+        const int64_t r0 = (int64_t)(c / G) * 32, r1 = std::min<int64_t>(s.q_len, r0 + 32);
+        pairs += (r1 - r0) * (s.ctx_len + 1) + (r0 + r1 - 1) * (r1 - r0) / 2;   // row r sees ctx + r + 1 keys
+      }
+      out.push_back({WorkItem{kItemPrefill | (w << 8), i, h, s.q_row_start, s.ctx_len, s.q_len, 0, 0}, kend, pairs});
+    }
+}
+
+// Mixed launch, page-balanced: workgroups [0, kd) stream equal key shares of
+// the decode sequences while the other CUs run the prefill items one after
+// another.  kd balances the two with a cost model fitted to per-workgroup
+// timestamps of config (d) and decode-only launches on MI355X (one 8-wave
+// workgroup per CU): k decode workgroups together stream 5.7 (1 - e^(-k / 57))
+// TB/s of a bf16 cache (measured 3.7, 5.3, 5.6 TB/s at k = 64, 128, 256); a
+// prefill item computes 4 D flops per (row, key) pair at ~4.2 TFLOP/s per CU
+// at D = 128 (3.0 assumed at D = 64), and the prefill CUs end up to half the
+// longest item apart.  kd is a multiple of 8 (the same on every XCD) and
+// leaves CUs on every XCD for prefill.
+int64_t mixed_decode_wgs(const gllm_attn_plan* p, int cus, int heads_req, const std::vector<PrefillPiece>& pcs) {
+  const BalancedShape sh = balanced_shape(p, cus, heads_req);
+  if (sh.units == 0) return 1;
+  const double dec_bytes = (double)sh.units * 16 * sh.hw * p->D * 2 * 2;
+  const double rate = p->D == 128 ? 4.2e12 : 3.0e12;
+  double pf_total = 0, pf_max = 0;
+  for (const PrefillPiece& pc : pcs) {
+    const double t = 4.0 * p->D * (double)pc.pairs / rate;
+    pf_total += t;
+    pf_max = std::max(pf_max, t);
+  }
+  const int step = cus >= 16 && cus % 8 == 0 ? 8 : 1;
+  int64_t best = 0;
+  double best_t = 0;
+  for (int64_t kd = step; kd <= cus - step; kd += step) {
+    const double td = dec_bytes / (5.7e12 * (1.0 - std::exp(-(double)kd / 57.0)));
+    const double tp = pf_total / (double)(cus - kd) + 0.5 * pf_max;
+    const double t = std::max(td, tp);
+    if (best == 0 || t < best_t) {
+      best = kd;
+      best_t = t;
+    }
+  }
+  return std::min<int64_t>(std::max<int64_t>(best, 1), sh.units);
+}
+
+// Prefill items of a mixed page-balanced launch; they follow its kd decode
+// workgroups, so with kd a multiple of 8 item j runs on XCD j % 8.  The
+// items of one (sequence, kv head) read the same K/V tiles: they go to one
+// XCD, next to each other, so they run together and read each tile from that
+// XCD's L2 instead of HBM.  Bundles, largest first, go to the XCD with the
+// least prefill work so far; each XCD runs its bundles in that order, a
+// bundle's items largest first.
+void plan_mixed_prefill(gllm_attn_plan* p, const std::vector<PrefillPiece>& pcs) {
+  constexpr int NX = 8;
+  struct Bundle { int64_t work; std::vector<const PrefillPiece*> items; };
+  std::vector<Bundle> bundles;
+  for (size_t i = 0; i < pcs.size();) {   // pieces come grouped by (sequence, kv head)
+    Bundle bu{0, {}};
+    size_t j = i;
+    for (; j < pcs.size() && pcs[j].it.seq == pcs[i].it.seq && pcs[j].it.a == pcs[i].it.a; ++j) {
+      bu.work += pcs[j].pairs;
+      bu.items.push_back(&pcs[j]);
+    }
+    std::stable_sort(bu.items.begin(), bu.items.end(),
+                     [](const PrefillPiece* x, const PrefillPiece* y) { return x->pairs > y->pairs; });
+    bundles.push_back(std::move(bu));
+    i = j;
+  }
+  std::stable_sort(bundles.begin(), bundles.end(), [](const Bundle& x, const Bundle& y) { return x.work > y.work; });
+  std::vector<std::vector<const PrefillPiece*>> q(NX);
+  std::vector<int64_t> load(NX, 0);
+  for (const Bundle& bu : bundles) {
+    int x = 0;
+    for (int y = 1; y < NX; ++y)
+      if (load[y] < load[x]) x = y;
+    q[x].insert(q[x].end(), bu.items.begin(), bu.items.end());
+    load[x] += bu.work;
+  }
+  p->items.clear();
+  p->items.reserve(pcs.size());
+  for (size_t k = 0; p->items.size() < pcs.size(); ++k)
+    for (int x = 0; x < NX; ++x)
+      if (k < q[x].size()) p->items.push_back(q[x][k]->it);
+  p->prefill_waves = 8;
 }
 
 }  // namespace
@@ -543,18 +654,35 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
     int64_t n_pf = 0;
     for (int i = 0; i < num_seqs; ++i)
       if ((int64_t)query_lens[i] * G > 16) ++n_pf;
-    if (split_tokens == GLLM_SPLIT_BALANCED && n_pf > 0) {
-      delete p;
-      return fail(GLLM_ATTN_EINVAL, "GLLM_SPLIT_BALANCED plans decode-only batches (%lld prefill-path sequences)",
-                  (long long)n_pf);
-    }
-    bool balanced = split_tokens == GLLM_SPLIT_BALANCED && num_seqs > 0;
-    if (n_pf == 0 && split_tokens == 0 && num_seqs > 0) {
+    bool balanced = false;
+    std::vector<PrefillPiece> pcs;   // prefill items of a mixed page-balanced launch
+    int64_t mixed_wgs = 0;
+    if (n_pf > 0) {
+      // Mixed batch, page-balanced decode share plus prefill items: on
+      // request only (config (d): 482-487 µs against 455-464 for the item plan
+      // below; 291 vs 299 µs with 128 decodes and 4 prefills).
+      if (n_pf < num_seqs && split_tokens == GLLM_SPLIT_BALANCED) {
+        for (int i = 0; i < num_seqs; ++i)
+          if (p->seqs[i].q_len * G > 16) prefill_pieces(p->seqs[i], i, G, num_kv_heads, pcs);
+        mixed_wgs = mixed_decode_wgs(p, cus, decode_heads_per_wg, pcs);
+        balanced = true;
+      }
+    } else if (split_tokens == GLLM_SPLIT_BALANCED) {
+      balanced = num_seqs > 0;
+    } else if (split_tokens == 0 && num_seqs > 0) {
       const BalancedShape bsh = balanced_shape(p, cus, decode_heads_per_wg);
       balanced = bsh.units >= balanced_min_units_per_wg(p->D) * bsh.wgs;
     }
     if (balanced) {
-      plan_balanced_decode(p, cus, decode_heads_per_wg);
+      plan_balanced_decode(p, cus, decode_heads_per_wg, mixed_wgs);
+      if (n_pf > 0) {
+        p->n_prefill_seqs = (int32_t)n_pf;
+        plan_mixed_prefill(p, pcs);
+        if (p->items.size() + p->seg_ptr.size() > (size_t)INT32_MAX) {
+          delete p;
+          return fail(GLLM_ATTN_EINVAL, "too many work items");
+        }
+      }
     } else {
     // Decode: one 8-wave workgroup per (sequence, split, HW kv heads); the
     // other 8 / HW waves interleave each head's keys.  Rule (fitted to MI355X
@@ -630,14 +758,9 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
           }
       } else {
         ++p->n_prefill_seqs;
-        const int nrb = (s.q_len + 31) / 32;
-        const int nwg = (G * nrb + pw - 1) / pw;
-        for (int h = 0; h < num_kv_heads; ++h)
-          for (int w = 0; w < nwg; ++w) {
-            const int last_combo = std::min(w * pw + pw - 1, G * nrb - 1);
-            const int64_t kend = s.ctx_len + std::min(s.q_len - 1, (last_combo / G) * 32 + 31) + 1;
-            pf.push_back({kend, WorkItem{kItemPrefill | (w << 8), i, h, s.q_row_start, s.ctx_len, s.q_len, 0, 0}});
-          }
+        pcs.clear();
+        prefill_pieces(s, i, G, num_kv_heads, pcs);
+        for (const PrefillPiece& pc : pcs) pf.push_back({pc.kend, pc.it});
       }
     }
     // Longest work first so the tail is made of short items.
@@ -664,22 +787,27 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
       }
       for (size_t k = m; k < ncu; ++k) all[k] = dc[k];   // middle items, alone on their CU
     } else {
-      // Prefill items (MFMA-bound) spread evenly through the decode items
-      // (HBM-bound): prefill item i goes before decode item i * ndc / npf, so
-      // at any time some CUs compute while the others keep HBM busy (a mixed
-      // launch holds one workgroup per CU).  Measured on config (d): 468 µs
-      // against 485 with all prefill items first and 512 with them last.
-      // Then snake order: alternate the direction every `cus` items, so each
-      // CU pairs long work with short.
+      // Mixed batch: the prefill items (MFMA-bound, longest first) are spread
+      // evenly through the first half of the decode items (HBM-bound, longest
+      // first): prefill item i goes before decode item i * ndc / (2 npf).
+      // Some CUs compute while the others keep HBM busy (a mixed launch holds
+      // one workgroup per CU), every prefill item has started by the middle
+      // of the launch, and the short decode items fill the tail.  Measured on
+      // config (d), mean of 8 runs each: 460 µs, against 469 with the prefill
+      // items spread through all the decode items, 464 / 463 with them in the
+      // first 40% / 30%, 485 with all of them first and 512 with them last.
+      // Decode-only item plans: snake order, the direction alternating every
+      // `cus` items, so each CU pairs long work with short.
       size_t di = 0;
       for (size_t i = 0; i < pf.size(); ++i) {
-        const size_t upto = i * dc.size() / pf.size();
+        const size_t upto = i * dc.size() / (2 * pf.size());
         while (di < upto) all.push_back(dc[di++]);
         all.push_back(pf[i]);
       }
       while (di < dc.size()) all.push_back(dc[di++]);
-      for (size_t c0 = ncu, chunk = 1; c0 < all.size(); c0 += ncu, ++chunk)
-        if (chunk & 1) std::reverse(all.begin() + c0, all.begin() + std::min(all.size(), c0 + ncu));
+      if (pf.empty())
+        for (size_t c0 = ncu, chunk = 1; c0 < all.size(); c0 += ncu, ++chunk)
+          if (chunk & 1) std::reverse(all.begin() + c0, all.begin() + std::min(all.size(), c0 + ncu));
     }
     p->items.reserve(all.size());
     for (auto& k : all) p->items.push_back(k.it);
@@ -731,7 +859,7 @@ size_t gllm_attn_plan_workspace_bytes(const gllm_attn_plan* p) { return p ? p->w
 
 int gllm_attn_plan_info(const gllm_attn_plan* p, int64_t* info, int32_t n) {
   if (!p || !info) return fail(GLLM_ATTN_EINVAL, "null plan or info");
-  const int64_t n_wg = p->segs.empty() ? (int64_t)p->items.size() : (int64_t)p->seg_ptr.size() - 1;
+  const int64_t n_wg = (int64_t)p->items.size() + (p->segs.empty() ? 0 : (int64_t)p->seg_ptr.size() - 1);
   const int64_t v[10] = {n_wg, p->split_len, p->n_decode_seqs, p->n_prefill_seqs, p->n_partials,
                          p->total_rows, p->heads_per_wg, p->decode_waves, p->prefill_waves,
                          (int64_t)p->segs.size()};
@@ -825,7 +953,8 @@ int gllm_paged_attention(const gllm_attn_plan* p, const void* q, int64_t q_row_s
     a.segs = (const DecodeSeg*)(p->ws + p->off_segs);
     a.seg_ptr = (const int32_t*)(p->ws + p->off_segptr);
     a.n_segs = (int32_t)p->segs.size();
-    a.n_items = (int32_t)p->seg_ptr.size() - 1;
+    a.n_seg_wgs = (int32_t)p->seg_ptr.size() - 1;
+    a.n_items = a.n_seg_wgs + (int32_t)p->items.size();   // decode workgroups, then any prefill items
   }
   a.num_seqs = p->num_seqs;
   a.counters = (int32_t*)(p->ws + p->off_ctr);

@@ -74,6 +74,7 @@ struct AttnArgs {
   const DecodeSeg* segs;
   const int32_t* seg_ptr;
   int32_t n_segs;
+  int32_t n_seg_wgs;          // workgroups running segments; a mixed launch's prefill items follow them
   int32_t split_len;
   int32_t heads_per_wg;       // decode: kv heads per workgroup (1, 2, 4, 8)
   int32_t decode_waves;       // decode: waves per workgroup (8)

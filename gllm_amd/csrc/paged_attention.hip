@@ -1161,6 +1161,30 @@ decode_balanced_kernel(AttnArgs a) {
   }
 }
 
+// Mixed continuous batch, page-balanced: workgroups [0, n_seg_wgs) run equal
+// key shares of the decode sequences (segments, as decode_balanced_kernel);
+// each later workgroup runs one prefill item.  One 8-wave workgroup per CU
+// (the prefill path's LDS ring and registers).
+template <int D, int HW, bool KV8>
+__global__ void __launch_bounds__(64 * kWaves) mixed_balanced_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) char lds[MixedLds<D, true, true, kWaves>::kBytes];
+  __shared__ int ticket;
+  const int b = blockIdx.x;
+  if (b >= a.n_seg_wgs) {
+    const WorkItem it = a.items[b - a.n_seg_wgs];
+    prefill_wg<D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
+    return;
+  }
+  const int s0 = a.seg_ptr[b], s1 = a.seg_ptr[b + 1];
+  for (int s = s0; s < s1; ++s) {
+    if (s > s0) __syncthreads();
+    const DecodeSeg sg = a.segs[s];
+    const DecodeTask tk{sg.seq, sg.hg, sg.k0, sg.k1, sg.q_row_start, sg.ctx_len, sg.q_len,
+                        sg.nseg, sg.pbase, sg.ord, sg.ticket};
+    decode_task<D, HW, kWaves / HW, KV8>(a, tk, lds, &ticket);
+  }
+}
+
 // Prefill items only: one 8-wave workgroup per CU, a 4-stage ring.
 template <int D, bool KV8>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2)))
@@ -1208,10 +1232,25 @@ static hipError_t launch_decode_balanced(const AttnArgs& a, hipStream_t st) {
 }
 
 template <int D, bool KV8>
+static hipError_t launch_mixed_balanced(const AttnArgs& a, hipStream_t st) {
+  const dim3 grid(a.n_items);
+  switch (a.heads_per_wg) {
+    case 1: hipLaunchKernelGGL((mixed_balanced_kernel<D, 1, KV8>), grid, dim3(64 * kWaves), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((mixed_balanced_kernel<D, 2, KV8>), grid, dim3(64 * kWaves), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((mixed_balanced_kernel<D, 4, KV8>), grid, dim3(64 * kWaves), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((mixed_balanced_kernel<D, 8, KV8>), grid, dim3(64 * kWaves), 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int D, bool KV8>
 static hipError_t launch_paged_d(const AttnArgs& a, bool pf, bool dc, hipStream_t st) {
   const int hw = a.heads_per_wg, nw = a.decode_waves;
   if (a.n_segs > 0) {
-    if (pf || nw != kWaves) return hipErrorInvalidValue;
+    if (nw != kWaves || (pf && a.prefill_waves != kWaves) || a.n_seg_wgs <= 0 || a.n_seg_wgs > a.n_items)
+      return hipErrorInvalidValue;
+    if (pf) return dc ? launch_mixed_balanced<D, KV8>(a, st) : hipErrorInvalidValue;
     return launch_decode_balanced<D, KV8>(a, st);
   }
   if (pf && (a.prefill_waves != kWaves || (dc && nw != kWaves)))

@@ -256,7 +256,7 @@ def build_metadata(block_table: torch.Tensor, seq_lens: torch.Tensor, query_lens
     return slots, pos, cu
 
 
-# split_tokens value that asks for a page-balanced decode plan
+# split_tokens value that asks for a page-balanced decode plan (decode-only or mixed batches)
 BALANCED = -1
 
 
@@ -267,7 +267,8 @@ class AttentionPlan:
     ``q_seq_stride`` > 0: sequence i's rows start at ``i * q_seq_stride`` (the
     reference's padded ``[B, T_q]`` layout); 0: packed rows.  ``split_tokens``:
     0 lets the planner choose, a multiple of 32 fixes the decode split length,
-    ``BALANCED`` deals a decode-only batch's keys evenly to the workgroups.
+    ``BALANCED`` deals the decode sequences' keys evenly to the workgroups (in
+    a mixed batch: to part of the CUs, the prefill items run on the rest).
     """
 
     def __init__(self, query_lens, seq_lens, *, num_q_heads: int, num_kv_heads: int, head_dim: int,

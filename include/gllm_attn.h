@@ -190,11 +190,14 @@ int gllm_rope_kv_write(const void* q, void* q_out, const void* k, const void* v,
  * per decode split (multiple of 32) and decode_heads_per_wg = kv heads one
  * decode workgroup serves (1, 2, 4 or 8); 0 lets the planner choose both from
  * the batch and the CU count.  split_tokens == GLLM_SPLIT_BALANCED (-1) plans
- * a decode-only batch page-balanced: its keys (16-key units per sequence and
- * kv-head group) are dealt out evenly to one workgroup per resident CU slot,
- * and sequences spread over several workgroups are merged inside the same
- * launch (split tickets); 0 picks it for decode-only batches whose workgroups
- * would each stream >= 2048 keys.  No device work happens here.
+ * the decode sequences page-balanced: their keys (16-key units per sequence
+ * and kv-head group) are dealt out evenly to one workgroup per resident CU
+ * slot, and sequences spread over several workgroups are merged inside the
+ * same launch (split tickets); 0 picks it for decode-only batches whose
+ * workgroups would each stream >= 2048 keys.  In a mixed batch (only on
+ * request) the decode share goes to a multiple of 8 workgroups sized by a
+ * cost model, and one workgroup per prefill item follows them on the other
+ * CUs.  No device work happens here.
  */
 int gllm_attn_plan_create(gllm_attn_plan** plan, const int32_t* query_lens,
                           const int32_t* seq_lens, int32_t num_seqs, int64_t q_seq_stride,

@@ -102,9 +102,17 @@ def test_planner_page_balanced():
     assert rc == 0 and i["segs"] == 0
     rc, i = _plan_info(lib, [1] * 256, [192 * 16] * 256, 32, 8, 128)
     assert rc == 0 and i["segs"] == 256 and i["wgs"] == 256
-    # prefill-path sequences cannot be planned page-balanced
-    rc, _ = _plan_info(lib, [1, 40], [100, 80], 32, 8, 64, split=-1)
-    assert rc == _lib.EINVAL and b"decode-only" in lib.gllm_attn_last_error()
+    # mixed batch, page-balanced on request: decode workgroups (a multiple of
+    # 8, one per CU) plus one workgroup per prefill item; auto keeps the item plan
+    rc, i = _plan_info(lib, d.q_lens, d.seq_lens, 32, 8, 128, split=-1)
+    assert rc == 0 and i["npf"] == 4 and i["ndec"] == 256 and i["segs"] > 0
+    kd = i["wgs"] - 4 * 8 * 8                       # 4 sequences x 8 kv heads x 8 items
+    assert 0 < kd < 256 and kd % 8 == 0
+    rc, i = _plan_info(lib, d.q_lens, d.seq_lens, 32, 8, 128)
+    assert rc == 0 and i["segs"] == 0 and i["wgs"] == 4 * 8 * 8 + 256 * 8 // i["hw"]
+    # a lone decode next to a prefill: one decode workgroup of one unit
+    rc, i = _plan_info(lib, [1, 40], [10, 80], 32, 8, 64, split=-1)
+    assert rc == 0 and (i["ndec"], i["npf"], i["segs"]) == (1, 1, 1)
 
 
 @pytest.mark.parametrize("args,code", [

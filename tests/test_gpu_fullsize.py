@@ -124,12 +124,17 @@ def test_config_c_prefill_full():
     assert_close_bf16(got, ref, "config c sampled rows")
 
 
-def test_config_d_mixed_full():
-    print("config d full", flush=True)
+@pytest.mark.parametrize("split", [0, paged.BALANCED])
+def test_config_d_mixed_full(split):
+    """Config (d) in one launch: the item plan, and the page-balanced decode
+    share with prefill items (twice: the split tickets are re-armed)."""
+    print(f"config d full split={split}", flush=True)
     b = workloads.materialize(workloads.config_d(), DEV, values_on_device=True)
-    plan = _plan(b)
+    plan = _plan(b, split_tokens=split)
     assert plan.info["decode_seqs"] == 256 and plan.info["prefill_seqs"] == 4
-    out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
+    assert (plan.info["decode_segments"] > 0) == (split == paged.BALANCED)
+    for _ in range(2 if split else 1):
+        out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
     torch.cuda.synchronize()
     g = torch.Generator().manual_seed(10)
     pairs = [(i, 0) for i in torch.randint(0, 256, (48,), generator=g).tolist()]

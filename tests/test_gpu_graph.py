@@ -21,6 +21,9 @@ CASES = {
     "decode_balanced": dict(ctx=[4000, 33, 2500, 700, 90], ql=[1] * 5, Hq=32, Hkv=8, D=64, split=paged.BALANCED),
     # mixed continuous batch: decodes plus two prefill chunks
     "mixed": dict(ctx=[700, 0, 250, 40], ql=[1, 90, 1, 33], Hq=32, Hkv=8, D=128, split=0),
+    # mixed, page-balanced decode share: tickets re-armed inside the graph
+    "mixed_balanced": dict(ctx=[4000, 0, 2500, 40, 900], ql=[1, 90, 1, 33, 1], Hq=32, Hkv=8, D=128,
+                           split=paged.BALANCED),
 }
 
 

@@ -230,23 +230,27 @@ def test_prefill_rope_in_kernel_matches_prerotated():
 
 
 # ------------------------------------------------------------ (d) mixed launch
-def test_mixed_batch_one_launch():
-    print("mixed", flush=True)
+@pytest.mark.parametrize("split", [256, paged.BALANCED])
+def test_mixed_batch_one_launch(split):
+    print(f"mixed split={split}", flush=True)
     ctx = [100, 0, 2000, 513, 64, 1000]
     ql = [1, 96, 1, 64, 1, 33]
     b = make_batch(ctx, ql, 32, 8, 128)
     plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=32, num_kv_heads=8, head_dim=128,
-                               block_size=16, dtype=torch.bfloat16, device=DEV, split_tokens=256)
+                               block_size=16, dtype=torch.bfloat16, device=DEV, split_tokens=split)
     info = plan.info
     assert info["decode_seqs"] == 3 and info["prefill_seqs"] == 3
-    out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
-    torch.cuda.synchronize()
-    assert_close_bf16(out, oracle_paged(b), "mixed")
+    assert (info["decode_segments"] > 0) == (split == paged.BALANCED)
+    ref = oracle_paged(b)
+    for rep in range(2):   # the second launch finds the split tickets re-armed
+        out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
+        torch.cuda.synchronize()
+        assert_close_bf16(out, ref, f"mixed rep {rep}")
 
 
 # ------------------------------------------------------------ block sizes
 @pytest.mark.parametrize("bs", [1, 3, 12, 24, 48, 100, 1000])
-@pytest.mark.parametrize("D,split", [(64, 0), (128, 96)])
+@pytest.mark.parametrize("D,split", [(64, 0), (128, 96), (64, paged.BALANCED), (128, paged.BALANCED)])
 def test_any_block_size_mixed(bs, D, split):
     """Block sizes that are not powers of two (the reference takes any
     size): one mixed launch with decodes (split and unsplit), prefill chunks

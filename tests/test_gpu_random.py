@@ -49,6 +49,8 @@ def _case(k):
     rope = r.random() < 0.5
     split = r.choice([0, 0, 32, 96, 256, paged.BALANCED]) if decode_only else 0
     hw = r.choice([0, 0, 1, 2, 4, 8])
+    if not decode_only and r.random() < 0.35:
+        split = paged.BALANCED   # mixed page-balanced plan (prefill items after the decode share)
     return dict(Hq=Hkv * G, Hkv=Hkv, D=D, bs=bs, kv8=kv8, ctx=ctx, ql=ql, rope=rope, split=split, hw=hw)
 
 
@@ -60,8 +62,6 @@ def test_random_batch(k):
     if c["kv8"]:
         b.k_cache, b.v_cache = b.k_cache.to(F8), b.v_cache.to(F8)
     split = c["split"]
-    if split == paged.BALANCED and any(q * (c["Hq"] // c["Hkv"]) > 16 for q in c["ql"]):
-        split = 0
     plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=c["Hq"], num_kv_heads=c["Hkv"], head_dim=c["D"],
                                block_size=c["bs"], dtype=torch.bfloat16, device=DEV, split_tokens=split,
                                heads_per_wg=c["hw"])
