@@ -30,13 +30,16 @@ template <> __device__ __forceinline__ void stq<__bf16>(__bf16* p, float x) {
 // a time, chunk c to wave c % 4: lane j scores key p0 + j against q (q read
 // from LDS, so every lane has all of it), one wave max / sum per chunk
 // updates the wave's exact online softmax (expf), then the lanes switch to
-// the head dims (d = lane + 64 i) and accumulate the chunk's p-weighted V
-// rows, 32 keys' rows loaded at once, each key's p and slot read out of its
-// lane.  The four waves' (max, sum, acc) merge through LDS at the end.
-template <bool DENSE, typename KV, typename QT>
+// the head dims (d = lane + 64 i, i < NI) and accumulate the chunk's
+// p-weighted V rows, each key's p and slot read out of its lane.  NI = 1
+// (D <= 64): the chunk's 64 V rows (one value per lane each) are loaded
+// before its K rows, so K and V arrive in one memory round trip; NI = 4: 32
+// keys' V rows per batch of loads, after the scores.  The four waves' (max,
+// sum, acc) merge through LDS at the end.
+template <bool DENSE, typename KV, typename QT, int NI>
 __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
   constexpr int NWV = 4;                  // waves per workgroup
-  constexpr int VB = 32;                  // V rows per batch of loads
+  constexpr int VB = NI == 1 ? 64 : 32;   // V rows per batch of loads
   __shared__ __attribute__((aligned(16))) float qs[256];
   __shared__ float mrg[NWV][2 + 256];     // per wave: max, sum, acc[D]
   const int hq = blockIdx.x, r = blockIdx.y, b = blockIdx.z;
@@ -92,10 +95,13 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
   const QT* brow = DENSE ? (const QT*)a.bias + (int64_t)b * a.bias_batch_stride + (int64_t)r * a.bias_row_stride
                          : nullptr;
   float m = kNegInf, l = 0.f;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float acc[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) acc[i] = 0.f;
   for (int p0 = 64 * wave; p0 < nkeys; p0 += 64 * NWV) {
     const int p = p0 + lane;
     const bool valid = p < nkeys;
+    const int nk = min(64, nkeys - p0);
     // row of key p in k (dense) or in the paged cache
     int64_t row = 0;
     if (valid) {
@@ -108,6 +114,24 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
         row = (int64_t)blk * a.block_size + (p - (int)bi * a.block_size);
       }
     }
+    const int rlo = (int)(uint32_t)row, rhi = (int)((uint64_t)row >> 32);
+    // V rows of key j (keys past the chunk re-read its last row, weight 0)
+    auto load_v = [&](int j0, float (&vv)[VB][NI]) {
+#pragma unroll
+      for (int u = 0; u < VB; ++u) {
+        const int j = min(j0 + u, nk - 1);
+        const int64_t rj = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane(rhi, j) << 32) |
+                                     (uint32_t)__builtin_amdgcn_readlane(rlo, j));
+        const KV* vp = vbase + rj * vstride;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const int d = lane + 64 * i;
+          vv[u][i] = d < D ? ldkv<KV>(vp + d) : 0.f;
+        }
+      }
+    };
+    float vpre[NI == 1 ? VB : 1][NI];
+    if constexpr (NI == 1) load_v(0, vpre);
     float s = kNegInf;
     if (valid) {
       const KV* kp = kbase + row * kstride;
@@ -135,31 +159,26 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
     for (int off = 32; off >= 1; off >>= 1) es += __shfl_xor(es, off);
     l = l * alpha + es;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] *= alpha;
-    const int nk = min(64, nkeys - p0);
-    const int rlo = (int)(uint32_t)row, rhi = (int)((uint64_t)row >> 32);
-    // VB keys' V rows loaded at once (keys past the chunk re-read its last
-    // row with weight 0), summed in key order
-    for (int j0 = 0; j0 < nk; j0 += VB) {
-      float pj[VB], vv[VB][4];
+    for (int i = 0; i < NI; ++i) acc[i] *= alpha;
+    // p-weighted V rows summed in key order
+    auto accumulate = [&](int j0, const float (&vv)[VB][NI]) {
 #pragma unroll
       for (int u = 0; u < VB; ++u) {
         const int j = min(j0 + u, nk - 1);
         const float pe = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(e), j));
-        pj[u] = j0 + u < nk ? pe : 0.f;
-        const int64_t rj = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane(rhi, j) << 32) |
-                                     (uint32_t)__builtin_amdgcn_readlane(rlo, j));
-        const KV* vp = vbase + rj * vstride;
+        const float pj = j0 + u < nk ? pe : 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int d = lane + 64 * i;
-          vv[u][i] = d < D ? ldkv<KV>(vp + d) : 0.f;
-        }
+        for (int i = 0; i < NI; ++i) acc[i] += pj * vv[u][i];
       }
-#pragma unroll
-      for (int u = 0; u < VB; ++u)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] += pj[u] * vv[u][i];
+    };
+    if constexpr (NI == 1) {
+      accumulate(0, vpre);
+    } else {
+      for (int j0 = 0; j0 < nk; j0 += VB) {
+        float vv[VB][NI];
+        load_v(j0, vv);
+        accumulate(j0, vv);
+      }
     }
     m = mn;
   }
@@ -170,7 +189,7 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
     mrg[wave][1] = l;
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NI; ++i) {
     const int d = lane + 64 * i;
     if (d < D) mrg[wave][2 + d] = acc[i];
   }
@@ -187,7 +206,7 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
   }
   QT* op = (QT*)a.out + qrow * a.out_row_stride + (int64_t)hq * D;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NI; ++i) {
     const int d = lane + 64 * i;
     if (d < D) {
       float o = 0.f;
@@ -198,25 +217,35 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
   }
 }
 
-hipError_t launch_attention_f32(const AttnArgs& a, bool dense, int B, int max_q, hipStream_t st) {
-  if (B == 0 || max_q == 0) return hipSuccess;
-  dim3 grid(a.num_q_heads, max_q, B), block(256);
+template <int NI>
+static void launch_f32_ni(const AttnArgs& a, bool dense, dim3 grid, hipStream_t st) {
+  const dim3 block(256);
   if (a.dtype == kBF16) {                 // bf16 model (head dims the MFMA kernels do not take)
     if (dense)
-      hipLaunchKernelGGL((attn_f32_kernel<true, __bf16, __bf16>), grid, block, 0, st, a);
+      hipLaunchKernelGGL((attn_f32_kernel<true, __bf16, __bf16, NI>), grid, block, 0, st, a);
     else if (a.kv_dtype == kFP8)
-      hipLaunchKernelGGL((attn_f32_kernel<false, fp8e4m3, __bf16>), grid, block, 0, st, a);
+      hipLaunchKernelGGL((attn_f32_kernel<false, fp8e4m3, __bf16, NI>), grid, block, 0, st, a);
     else
-      hipLaunchKernelGGL((attn_f32_kernel<false, __bf16, __bf16>), grid, block, 0, st, a);
+      hipLaunchKernelGGL((attn_f32_kernel<false, __bf16, __bf16, NI>), grid, block, 0, st, a);
   } else if (dense) {
-    hipLaunchKernelGGL((attn_f32_kernel<true, float, float>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((attn_f32_kernel<true, float, float, NI>), grid, block, 0, st, a);
   } else if (a.kv_dtype == kF32) {
-    hipLaunchKernelGGL((attn_f32_kernel<false, float, float>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((attn_f32_kernel<false, float, float, NI>), grid, block, 0, st, a);
   } else if (a.kv_dtype == kFP8) {
-    hipLaunchKernelGGL((attn_f32_kernel<false, fp8e4m3, float>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((attn_f32_kernel<false, fp8e4m3, float, NI>), grid, block, 0, st, a);
   } else {
-    hipLaunchKernelGGL((attn_f32_kernel<false, __bf16, float>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((attn_f32_kernel<false, __bf16, float, NI>), grid, block, 0, st, a);
   }
+}
+
+hipError_t launch_attention_f32(const AttnArgs& a, bool dense, int B, int max_q, hipStream_t st) {
+  if (B == 0 || max_q == 0) return hipSuccess;
+  if (a.head_dim <= 0 || a.head_dim > 256) return hipErrorInvalidValue;
+  const dim3 grid(a.num_q_heads, max_q, B);
+  if (a.head_dim <= 64)
+    launch_f32_ni<1>(a, dense, grid, st);
+  else
+    launch_f32_ni<4>(a, dense, grid, st);
   return hipGetLastError();
 }
 
