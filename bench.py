@@ -34,7 +34,7 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from gllm_amd import paged, workloads  # noqa: E402
+from gllm_amd import _lib, paged, workloads  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
@@ -318,16 +318,57 @@ def progress(what: str) -> None:
     print(f"[bench] {what}", file=sys.stderr, flush=True)
 
 
+def _probe_lib():
+    """libgllm_probe.so (built beside the attention library by gllm_amd.build):
+    the read-stream and L2 -> LDS copy probes of the box ceilings."""
+    import ctypes
+    from gllm_amd import build as gb
+    lib = ctypes.CDLL(gb.PROBE_LIB)
+    p, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    lib.gllm_probe_read.argtypes = [p, i64, i32, p, p]
+    lib.gllm_probe_lds_dma.argtypes = [p, i64, i32, i32, p, p]
+    return lib
+
+
 def bench_box_ceilings(dev, warmup, reps):
-    """What this box's library kernels reach on plain patterns, as context
-    for the roofline fractions (not the peaks they are priced against): a
-    device copy of 2 GiB (torch's copy kernel; bytes read + written) and a
-    bf16 8192^3 GEMM (torch.mm -> hipBLASLt)."""
+    """What this box reaches on plain patterns, as context for the roofline
+    fractions (not the peaks they are priced against): a device copy of 2 GiB
+    (torch's copy kernel; bytes read + written), a read-only stream of 8 GiB
+    (16-byte loads, 8 per lane in flight, 4 workgroups per CU; far above the
+    256 MB MALL, so HBM), an L2-resident 2 MiB window copied into LDS rings
+    with global_load_lds_dwordx4 (the prefill K/V ring's load path; 2
+    workgroups per CU, no compute) and a bf16 8192^3 GEMM (torch.mm ->
+    hipBLASLt)."""
     src = torch.empty(1 << 30, dtype=torch.bfloat16, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
     per, _ = graph_reps([lambda: dst.copy_(src)], warmup, reps, 1)
     copy_ms = statistics.median(per)
     del src, dst
+    lib = _probe_lib()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    rbytes = 8 << 30
+    wgs = 4 * cus
+    rbytes -= rbytes % (wgs * 32768)
+    buf = torch.empty(rbytes, dtype=torch.uint8, device=dev).fill_(1)
+    sink = torch.zeros(8 * cus, dtype=torch.int32, device=dev)
+
+    def read_once():
+        rc = lib.gllm_probe_read(buf.data_ptr(), rbytes, wgs, sink.data_ptr(), _lib.stream_ptr(dev))
+        if rc:
+            raise RuntimeError(f"gllm_probe_read: hip error {rc}")
+    per, _ = graph_reps([read_once], warmup, max(5, reps // 2), 1)
+    read_ms = statistics.median(per)
+    del buf
+    window, iters, lwgs = 2 << 20, 2048, 2 * cus
+    win = torch.empty(window, dtype=torch.uint8, device=dev).fill_(1)
+
+    def lds_once():
+        rc = lib.gllm_probe_lds_dma(win.data_ptr(), window, lwgs, iters, sink.data_ptr(), _lib.stream_ptr(dev))
+        if rc:
+            raise RuntimeError(f"gllm_probe_lds_dma: hip error {rc}")
+    per, _ = graph_reps([lds_once], warmup, max(5, reps // 2), 1)
+    lds_ms = statistics.median(per)
+    del win, sink
     a = torch.randn(8192, 8192, device=dev).to(torch.bfloat16)
     bm = torch.randn(8192, 8192, device=dev).to(torch.bfloat16)
     per, _ = graph_reps([lambda: torch.mm(a, bm)], warmup, max(5, reps // 4), 1)
@@ -335,7 +376,11 @@ def bench_box_ceilings(dev, warmup, reps):
     del a, bm
     torch.cuda.empty_cache()
     cb = 2 * (2 << 30)
+    lb = lwgs * iters * 4096
     return {"copy_2gib_gbs": cb / (copy_ms * 1e-3) / 1e9, "copy_frac_of_hbm_peak": cb / (copy_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "read_8gib_gbs": rbytes / (read_ms * 1e-3) / 1e9,
+            "read_frac_of_hbm_peak": rbytes / (read_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "l2_to_lds_2mib_tbs": lb / (lds_ms * 1e-3) / 1e12,
             "gemm_bf16_8192_tflops": 2 * 8192 ** 3 / (gemm_ms * 1e-3) / 1e12,
             "gemm_frac_of_mfma_peak": 2 * 8192 ** 3 / (gemm_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
 

@@ -3,7 +3,8 @@
     python -m gllm_amd.build        # or gllm_amd.build.build()
 
 Each .hip unit is compiled to an object in parallel, then linked into
-``gllm_amd/lib/libgllm_attn.so``.  Units whose arithmetic must round like the
+``gllm_amd/lib/libgllm_attn.so`` (the memory-path probes of bench.py's box
+ceilings into ``gllm_amd/lib/libgllm_probe.so``).  Units whose arithmetic must round like the
 reference's torch ops are compiled with ``-ffp-contract=off``.
 """
 from __future__ import annotations
@@ -22,6 +23,9 @@ ARCH = "gfx950"
 
 SOURCES = ["api.hip", "rope_kv_write.hip", "paged_attention.hip", "attention_f32.hip", "metadata.hip",
            "qkv_proj.hip"]
+# memory-path probes behind bench.py's box ceilings (own library, not the attention path)
+PROBE_SOURCES = ["probe.hip"]
+PROBE_LIB = os.path.join(LIBDIR, "libgllm_probe.so")
 NO_CONTRACT = {"rope_kv_write.hip", "attention_f32.hip", "qkv_proj.hip"}
 # MFMA accumulators stay in VGPRs (no per-tile AGPR<->VGPR copies)
 EXTRA = {"paged_attention.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"]}
@@ -45,22 +49,26 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(LIBDIR, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(4, os.cpu_count() or 1)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs,
-           # roctx ranges around the entry points
-           "-L/opt/rocm/lib", "-lrocprofiler-sdk-roctx", "-Wl,-rpath,/opt/rocm/lib"]
+def _link(objs, out, extra):
+    tmp = out + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, *extra]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr[-4000:]}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
     for o in objs:
         os.remove(o)
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(LIBDIR, exist_ok=True)
+    with ThreadPoolExecutor(max_workers=min(4, os.cpu_count() or 1)) as ex:
+        objs = list(ex.map(_compile, SOURCES + PROBE_SOURCES))
+    # roctx ranges around the entry points
+    _link(objs[:len(SOURCES)], LIB, ["-L/opt/rocm/lib", "-lrocprofiler-sdk-roctx", "-Wl,-rpath,/opt/rocm/lib"])
+    _link(objs[len(SOURCES):], PROBE_LIB, [])
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {PROBE_LIB}")
     return LIB
 
 
