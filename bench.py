@@ -327,6 +327,7 @@ def _probe_lib():
     p, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
     lib.gllm_probe_read.argtypes = [p, i64, i32, p, p]
     lib.gllm_probe_lds_dma.argtypes = [p, i64, i32, i32, p, p]
+    lib.gllm_probe_mfma.argtypes = [i32, i32, p, p]
     return lib
 
 
@@ -369,6 +370,16 @@ def bench_box_ceilings(dev, warmup, reps):
     per, _ = graph_reps([lds_once], warmup, max(5, reps // 2), 1)
     lds_ms = statistics.median(per)
     del win, sink
+    # one wave: cycles per 8 bf16 32x32x16 MFMAs, alone and with 64
+    # independent FMAs between them; shader clock of that wave
+    mf = torch.zeros(2, 4, dtype=torch.int64, device=dev)
+    for mode in (0, 1):
+        for _ in range(2):   # the second run is the one kept (clocks settled)
+            rc = lib.gllm_probe_mfma(mode, 4096, mf[mode].data_ptr(), _lib.stream_ptr(dev))
+            if rc:
+                raise RuntimeError(f"gllm_probe_mfma: hip error {rc}")
+            torch.cuda.synchronize()
+    mf = mf.cpu().tolist()
     a = torch.randn(8192, 8192, device=dev).to(torch.bfloat16)
     bm = torch.randn(8192, 8192, device=dev).to(torch.bfloat16)
     per, _ = graph_reps([lambda: torch.mm(a, bm)], warmup, max(5, reps // 4), 1)
@@ -381,6 +392,8 @@ def bench_box_ceilings(dev, warmup, reps):
             "read_8gib_gbs": rbytes / (read_ms * 1e-3) / 1e9,
             "read_frac_of_hbm_peak": rbytes / (read_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "l2_to_lds_2mib_tbs": lb / (lds_ms * 1e-3) / 1e12,
+            "mfma32x32x16_bf16_cycles_per_8": mf[0][0], "mfma_8_plus_64_fma_cycles": mf[1][0],
+            "one_wave_shader_clock_ghz": mf[0][0] * mf[0][3] / (mf[0][1] * 10.0),
             "gemm_bf16_8192_tflops": 2 * 8192 ** 3 / (gemm_ms * 1e-3) / 1e12,
             "gemm_frac_of_mfma_peak": 2 * 8192 ** 3 / (gemm_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
 

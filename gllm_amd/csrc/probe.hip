@@ -10,6 +10,8 @@
 //                       window into an LDS ring with global_load_lds_dwordx4,
 //                       NS - 1 steps in flight, no compute (the load path the
 //                       prefill kernel's K/V ring uses).
+//   gllm_probe_mfma:    one wave's cycles per 8 bf16 32x32x16 MFMAs, alone
+//                       or with 64 independent FMAs between them.
 #include "common.h"
 
 namespace gllm {
@@ -55,6 +57,54 @@ __global__ void __launch_bounds__(256) probe_lds_dma_kernel(const char* buf, int
   if (tid == 0) out[blockIdx.x] = *reinterpret_cast<const uint32_t*>(lds + 16 * (blockIdx.x & 7));
 }
 
+// One wave: `iters` groups of 8 v_mfma_f32_32x32x16_bf16 on one
+// accumulator, alone (mode 0) or with 64 independent fp32 FMAs (8 chains)
+// placed between them (mode 1); out[0] = shader-clock cycles per group
+// (s_memtime), out[1] = 100 MHz ticks of the whole loop (s_memrealtime), so
+// cycles / ticks gives the shader clock.  out[2..3] keep the results live.
+template <int MODE>
+__global__ void __launch_bounds__(64) probe_mfma_kernel(int iters, int64_t* out) {
+  const int lane = threadIdx.x;
+  bf16x8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = (__bf16)(0.001f * (lane + i));
+    b[i] = (__bf16)(0.002f * (lane - i));
+  }
+  f32x16 acc;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.f;
+  float x[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) x[c] = 1.f + 0.01f * (lane + c);
+  const float y = 0.999f, z = 0.001f;
+  const int64_t t0 = __builtin_amdgcn_s_memtime();
+  const int64_t r0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      acc = mfma32(a, b, acc);
+      if constexpr (MODE == 1) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) x[c] = __builtin_fmaf(x[c], y, z);
+      }
+    }
+  }
+  const int64_t t1 = __builtin_amdgcn_s_memtime();
+  const int64_t r1 = __builtin_amdgcn_s_memrealtime();
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) s += acc[j];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) s += x[c];
+  if (lane == 0) {
+    out[0] = (t1 - t0) / iters;
+    out[1] = r1 - r0;
+    out[2] = (int64_t)s;
+    out[3] = iters;
+  }
+}
+
 }  // namespace
 }  // namespace gllm
 
@@ -78,5 +128,15 @@ extern "C" int gllm_probe_lds_dma(const void* buf, int64_t window, int32_t wgs, 
     return (int)hipErrorInvalidValue;
   hipLaunchKernelGGL(probe_lds_dma_kernel<4>, dim3(wgs), dim3(256), 0, (hipStream_t)stream, (const char*)buf,
                      window - 1, iters, (uint32_t*)out);
+  return (int)hipGetLastError();
+}
+
+// mode 0: MFMAs alone, 1: with interleaved independent FMAs; out: 4 int64.
+extern "C" int gllm_probe_mfma(int32_t mode, int32_t iters, void* out, void* stream) {
+  if (!out || iters <= 0 || (mode != 0 && mode != 1)) return (int)hipErrorInvalidValue;
+  if (mode == 0)
+    hipLaunchKernelGGL(probe_mfma_kernel<0>, dim3(1), dim3(64), 0, (hipStream_t)stream, (int)iters, (int64_t*)out);
+  else
+    hipLaunchKernelGGL(probe_mfma_kernel<1>, dim3(1), dim3(64), 0, (hipStream_t)stream, (int)iters, (int64_t*)out);
   return (int)hipGetLastError();
 }
