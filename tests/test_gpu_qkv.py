@@ -7,6 +7,8 @@ rounding boundary (torch's own bf16 F.linear does the same); random-data
 cases allow that on a small fraction of values.  With small-integer data
 every dot product is exact in fp32 and bf16, so those cases pin the RoPE,
 the casts and the slot writes bit for bit."""
+import os
+
 import pytest
 import torch
 
@@ -289,7 +291,9 @@ def _random_shapes(count, seed):
     return out
 
 
-@pytest.mark.parametrize("n,hidden,Hq,Hkv,D,kvd,rotate_q,with_q", _random_shapes(16, 2024))
+# GLLM_QKV_RANDOM_SHAPES=n draws n seeded shapes instead of the default 16
+@pytest.mark.parametrize("n,hidden,Hq,Hkv,D,kvd,rotate_q,with_q",
+                         _random_shapes(int(os.environ.get("GLLM_QKV_RANDOM_SHAPES", "16")), 2024))
 def test_qkv_random_shapes_exact(n, hidden, Hq, Hkv, D, kvd, rotate_q, with_q):
     """Random shapes (seeded), small-integer data: every fused path is
     bit-exact against the oracle."""
