@@ -32,9 +32,10 @@ template <> __device__ __forceinline__ void stq<__bf16>(__bf16* p, float x) {
 // updates the wave's exact online softmax (expf), then the lanes switch to
 // the head dims (d = lane + 64 i, i < NI) and accumulate the chunk's
 // p-weighted V rows, each key's p and slot read out of its lane.  NI = 1
-// (D <= 64): the chunk's 64 V rows (one value per lane each) are loaded
-// before its K rows, so K and V arrive in one memory round trip; NI = 4: 32
-// keys' V rows per batch of loads, after the scores.  The four waves' (max,
+// (D <= 64, a multiple of 4): the chunk's 64 V rows (one value per lane
+// each) and then each lane's whole K row are loaded before any is used, so K
+// and V arrive in one memory round trip; NI = 4: 32 keys' V rows per batch
+// of loads, after the scores.  The four waves' (max,
 // sum, acc) merge through LDS at the end.
 template <bool DENSE, typename KV, typename QT, int NI>
 __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
@@ -83,6 +84,7 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
     }
     qs[d] = qv;
   }
+  for (int d = D + tid; d < 64 * NI; d += 64 * NWV) qs[d] = 0.f;   // dims past D score 0
   __syncthreads();
   const int nkeys = DENSE ? L : ctx + r + 1;
   const int32_t* bt = DENSE ? nullptr : a.block_table + (int64_t)b * a.block_table_stride;
@@ -124,9 +126,10 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
                                      (uint32_t)__builtin_amdgcn_readlane(rlo, j));
         const KV* vp = vbase + rj * vstride;
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
+        for (int i = 0; i < NI; ++i) {   // every lane loads (dims past D re-read dim D - 1): no branch per load
           const int d = lane + 64 * i;
-          vv[u][i] = d < D ? ldkv<KV>(vp + d) : 0.f;
+          const float v = ldkv<KV>(vp + min(d, D - 1));
+          vv[u][i] = d < D ? v : 0.f;
         }
       }
     };
@@ -136,14 +139,32 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
     if (valid) {
       const KV* kp = kbase + row * kstride;
       float dot = 0.f;
-      int d = 0;
+      if constexpr (NI == 1) {
+        // D <= 64, a multiple of 4: the whole row's loads are issued before
+        // any is used (16 chunks of 4 dims; chunks past D re-read the last
+        // one and meet q = 0), then summed chunk by chunk in dim order
+        float kv[16][4];
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+          const int cs = min(4 * c, D - 4);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) kv[c][j] = ldkv<KV>(kp + cs + j);
+        }
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+          const f32x4 qv = *reinterpret_cast<const f32x4*>(qs + 4 * c);
+          dot += qv[0] * kv[c][0] + qv[1] * kv[c][1] + qv[2] * kv[c][2] + qv[3] * kv[c][3];
+        }
+      } else {
+        int d = 0;
 #pragma unroll 16
-      for (; d + 4 <= D; d += 4) {                     // unrolled: the row's loads are in flight together
-        const f32x4 qv = *reinterpret_cast<const f32x4*>(qs + d);
-        dot += qv[0] * ldkv<KV>(kp + d) + qv[1] * ldkv<KV>(kp + d + 1) + qv[2] * ldkv<KV>(kp + d + 2) +
-               qv[3] * ldkv<KV>(kp + d + 3);
+        for (; d + 4 <= D; d += 4) {
+          const f32x4 qv = *reinterpret_cast<const f32x4*>(qs + d);
+          dot += qv[0] * ldkv<KV>(kp + d) + qv[1] * ldkv<KV>(kp + d + 1) + qv[2] * ldkv<KV>(kp + d + 2) +
+                 qv[3] * ldkv<KV>(kp + d + 3);
+        }
+        for (; d < D; ++d) dot += qs[d] * ldkv<KV>(kp + d);   // head dims not a multiple of 4
       }
-      for (; d < D; ++d) dot += qs[d] * ldkv<KV>(kp + d);   // head dims not a multiple of 4
       s = dot * a.scale;
       if (DENSE) s += (float)brow[p];
     }
@@ -242,7 +263,7 @@ hipError_t launch_attention_f32(const AttnArgs& a, bool dense, int B, int max_q,
   if (B == 0 || max_q == 0) return hipSuccess;
   if (a.head_dim <= 0 || a.head_dim > 256) return hipErrorInvalidValue;
   const dim3 grid(a.num_q_heads, max_q, B);
-  if (a.head_dim <= 64)
+  if (a.head_dim <= 64 && a.head_dim % 4 == 0)
     launch_f32_ni<1>(a, dense, grid, st);
   else
     launch_f32_ni<4>(a, dense, grid, st);
