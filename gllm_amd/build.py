@@ -1,6 +1,7 @@
 """Builds libgllm_attn.so (gfx950) in-tree with hipcc.
 
-    python -m gllm_amd.build        # or gllm_amd.build.build()
+    python -m gllm_amd.build                # or gllm_amd.build.build()
+    python -m gllm_amd.build --timestamps   # libgllm_attn_ts.so, for gllm_amd.timeline
 
 Each .hip unit is compiled to an object in parallel, then linked into
 ``gllm_amd/lib/libgllm_attn.so`` (the memory-path probes of bench.py's box
@@ -37,9 +38,12 @@ COMMON = [
 ]
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(LIBDIR, src.replace(".hip", ".o"))
-    cmd = [HIPCC, *COMMON, "-c", os.path.join(CSRC, src), "-o", obj]
+TS_LIB = os.path.join(LIBDIR, "libgllm_attn_ts.so")   # per-workgroup timestamp build (gllm_amd.timeline)
+
+
+def _compile(src: str, defines=()) -> str:
+    obj = os.path.join(LIBDIR, src.replace(".hip", "_ts.o" if defines else ".o"))
+    cmd = [HIPCC, *COMMON, *[f"-D{d}" for d in defines], "-c", os.path.join(CSRC, src), "-o", obj]
     if src in NO_CONTRACT:
         cmd.insert(1, "-ffp-contract=off")
     cmd[1:1] = EXTRA.get(src, [])
@@ -72,6 +76,21 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+def build_timestamps(verbose: bool = False) -> str:
+    """The attention library with per-workgroup timestamps
+    (-DGLLM_TIMESTAMPS) as libgllm_attn_ts.so, for ``gllm_amd.timeline``."""
+    os.makedirs(LIBDIR, exist_ok=True)
+    with ThreadPoolExecutor(max_workers=min(4, os.cpu_count() or 1)) as ex:
+        objs = list(ex.map(lambda src: _compile(src, ("GLLM_TIMESTAMPS",)), SOURCES))
+    _link(objs, TS_LIB, ["-L/opt/rocm/lib", "-lrocprofiler-sdk-roctx", "-Wl,-rpath,/opt/rocm/lib"])
+    if verbose:
+        print(f"built {TS_LIB}")
+    return TS_LIB
+
+
 if __name__ == "__main__":
-    build(verbose=True)
+    if "--timestamps" in sys.argv[1:]:
+        build_timestamps(verbose=True)
+    else:
+        build(verbose=True)
     sys.exit(0)

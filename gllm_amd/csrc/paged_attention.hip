@@ -25,6 +25,37 @@
 
 namespace gllm {
 
+// Per-workgroup timeline, only in the timestamp build (-DGLLM_TIMESTAMPS,
+// `python -m gllm_amd.build --timestamps`, read by gllm_amd/timeline.py):
+// thread 0 of each of the first 32768 workgroups of a launch records its
+// start and end (s_memrealtime, 100 MHz), its kind (0 decode item, 1 prefill
+// item, 2 decode segments) with the XCD it ran on, and its keys.  The record
+// is written when the kernel body returns, on every path.
+#ifdef GLLM_TIMESTAMPS
+__device__ long long gllm_ts_buf[4 << 15];
+struct WgStamp {
+  long long t0;
+  int kind = 0, keys = 0;
+  __device__ WgStamp() : t0(__builtin_amdgcn_s_memrealtime()) {}
+  __device__ ~WgStamp() {
+    if (threadIdx.x == 0 && blockIdx.x < (1u << 15)) {
+      unsigned x;
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+      long long* d = gllm_ts_buf + 4 * (int64_t)blockIdx.x;
+      d[0] = t0;
+      d[1] = __builtin_amdgcn_s_memrealtime();
+      d[2] = kind | (long long)((x & 15) << 8);
+      d[3] = keys;
+    }
+  }
+};
+#define GLLM_WG_STAMP(name) WgStamp name
+#define GLLM_WG_STAMP_SET(name, k, n) (name.kind = (k), name.keys = (n))
+#else
+#define GLLM_WG_STAMP(name)
+#define GLLM_WG_STAMP_SET(name, k, n) ((void)0)
+#endif
+
 // Rotate-half RoPE on 8 pairs, each op rounded to bf16 like the reference's
 // torch ops (gllm/model/layers/attention.py:105-118).
 __device__ __forceinline__ void rope8_bf16(float* x1, float* x2, const float* c, const float* s) {
@@ -1135,7 +1166,9 @@ __device__ __forceinline__ int xcd_item(int b, int n) {
 template <int D, bool PF, bool DC, int HW, int KW, bool KV8>
 __global__ void __launch_bounds__(64 * HW * KW) paged_attn_bf16_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[MixedLds<D, PF, DC, HW * KW>::kBytes];
+  GLLM_WG_STAMP(stamp);
   const WorkItem it = a.items[xcd_item<!PF && KV8 && HW * D < 128>(blockIdx.x, a.n_items)];
+  GLLM_WG_STAMP_SET(stamp, (it.kind_b & 0xff) == kItemPrefill ? 1 : 0, it.ctx_len + it.q_len);
   if (PF && (!DC || (it.kind_b & 0xff) == kItemPrefill)) {
     if constexpr (HW * KW == kWaves)
       prefill_wg<D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
@@ -1151,7 +1184,9 @@ __global__ void __launch_bounds__(64 * HW * KW) __attribute__((amdgpu_waves_per_
 decode_balanced_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[DecodeCfg<D, HW * KW>::kLdsBytes];
   __shared__ int ticket;
+  GLLM_WG_STAMP(stamp);
   const int s0 = a.seg_ptr[blockIdx.x], s1 = a.seg_ptr[blockIdx.x + 1];
+  GLLM_WG_STAMP_SET(stamp, 2, s1 - s0);
   for (int s = s0; s < s1; ++s) {
     if (s > s0) __syncthreads();
     const DecodeSeg sg = a.segs[s];
@@ -1169,13 +1204,16 @@ template <int D, int HW, bool KV8>
 __global__ void __launch_bounds__(64 * kWaves) mixed_balanced_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[MixedLds<D, true, true, kWaves>::kBytes];
   __shared__ int ticket;
+  GLLM_WG_STAMP(stamp);
   const int b = blockIdx.x;
   if (b >= a.n_seg_wgs) {
     const WorkItem it = a.items[b - a.n_seg_wgs];
+    GLLM_WG_STAMP_SET(stamp, 1, it.ctx_len + it.q_len);
     prefill_wg<D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
     return;
   }
   const int s0 = a.seg_ptr[b], s1 = a.seg_ptr[b + 1];
+  GLLM_WG_STAMP_SET(stamp, 2, s1 - s0);
   for (int s = s0; s < s1; ++s) {
     if (s > s0) __syncthreads();
     const DecodeSeg sg = a.segs[s];
@@ -1190,7 +1228,9 @@ template <int D, bool KV8>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2)))
 prefill_bf16_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[PrefillCfg<D, kPrefillStages>::kLdsBytes];
+  GLLM_WG_STAMP(stamp);
   const WorkItem it = a.items[blockIdx.x];
+  GLLM_WG_STAMP_SET(stamp, 1, it.ctx_len + it.q_len);
   prefill_wg<D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
 }
 
@@ -1312,3 +1352,12 @@ hipError_t launch_fill_zero_i32(int32_t* p, int64_t n, hipStream_t st) {
 }
 
 }  // namespace gllm
+
+#ifdef GLLM_TIMESTAMPS
+// Copies the timeline records of the last instrumented launch (4 int64 per
+// workgroup) to host memory; returns a hipError_t code.
+extern "C" int gllm_debug_timestamps(void* host, size_t bytes) {
+  if (bytes > sizeof(gllm::gllm_ts_buf)) bytes = sizeof(gllm::gllm_ts_buf);
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(gllm::gllm_ts_buf), bytes, 0, hipMemcpyDeviceToHost);
+}
+#endif
