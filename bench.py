@@ -328,6 +328,7 @@ def _probe_lib():
     lib.gllm_probe_read.argtypes = [p, i64, i32, p, p]
     lib.gllm_probe_lds_dma.argtypes = [p, i64, i32, i32, p, p]
     lib.gllm_probe_mfma.argtypes = [i32, i32, p, p]
+    lib.gllm_probe_empty.argtypes = [i32, i32, i32, p, p]
     return lib
 
 
@@ -367,20 +368,32 @@ def _probe_ceilings(lib, dev, warmup, reps):
                 raise RuntimeError(f"gllm_probe_mfma: hip error {rc}")
             torch.cuda.synchronize()
     mf = mf.cpu().tolist()
+    # launch cost of config (b)'s grid shape (512 workgroups of 512 threads,
+    # 33 KB of LDS each), doing nothing: per node of a 32-node graph
+    dummy = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def empty_once():
+        rc = lib.gllm_probe_empty(512, 512, 33 * 1024, dummy.data_ptr(), _lib.stream_ptr(dev))
+        if rc:
+            raise RuntimeError(f"gllm_probe_empty: hip error {rc}")
+    per, _ = graph_reps([empty_once], warmup, max(5, reps // 2), 32)
+    empty_us = statistics.median(per) * 1e3
     torch.cuda.empty_cache()
     return {"read_8gib_gbs": rbytes / (read_ms * 1e-3) / 1e9,
             "read_frac_of_hbm_peak": rbytes / (read_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "l2_to_lds_2mib_tbs": lwgs * iters * 4096 / (lds_ms * 1e-3) / 1e12,
             "mfma32x32x16_bf16_cycles_per_8": mf[0][0], "mfma_8_plus_64_fma_cycles": mf[1][0],
-            "one_wave_shader_clock_ghz": mf[0][0] * mf[0][3] / (mf[0][1] * 10.0)}
+            "one_wave_shader_clock_ghz": mf[0][0] * mf[0][3] / (mf[0][1] * 10.0),
+            "empty_512x512_graph_us": empty_us}
 
 
 def bench_box_ceilings(dev, warmup, reps):
     """What this box reaches on plain patterns, as context for the roofline
     fractions (not the peaks they are priced against): a device copy of 2 GiB
     (torch's copy kernel; bytes read + written), the probes of
-    ``_probe_ceilings`` (skipped with a note if libgllm_probe.so is absent)
-    and a bf16 8192^3 GEMM (torch.mm -> hipBLASLt)."""
+    ``_probe_ceilings`` (skipped with a note if libgllm_probe.so is absent),
+    the time per graph node of a one-element kernel (the launch floor of a
+    graph-replayed step) and a bf16 8192^3 GEMM (torch.mm -> hipBLASLt)."""
     src = torch.empty(1 << 30, dtype=torch.bfloat16, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
     per, _ = graph_reps([lambda: dst.copy_(src)], warmup, reps, 1)
@@ -396,6 +409,11 @@ def bench_box_ceilings(dev, warmup, reps):
         lib = None
     if lib is not None:
         out.update(_probe_ceilings(lib, dev, warmup, reps))
+    # launch floor: a one-element kernel per graph node, 32 nodes per graph
+    one = torch.zeros(1, device=dev)
+    per, _ = graph_reps([lambda: one.add_(1.0)], warmup, max(5, reps // 2), 32)
+    out["tiny_kernel_graph_us"] = statistics.median(per) * 1e3
+    del one
     a = torch.randn(8192, 8192, device=dev).to(torch.bfloat16)
     bm = torch.randn(8192, 8192, device=dev).to(torch.bfloat16)
     per, _ = graph_reps([lambda: torch.mm(a, bm)], warmup, max(5, reps // 4), 1)

@@ -12,6 +12,7 @@
 //                       prefill kernel's K/V ring uses).
 //   gllm_probe_mfma:    one wave's cycles per 8 bf16 32x32x16 MFMAs, alone
 //                       or with 64 independent FMAs between them.
+//   gllm_probe_empty:   a grid of workgroups that do nothing (launch cost).
 #include "common.h"
 
 namespace gllm {
@@ -105,6 +106,13 @@ __global__ void __launch_bounds__(64) probe_mfma_kernel(int iters, int64_t* out)
   }
 }
 
+// Workgroups that do nothing but take their LDS: the cost of launching and
+// retiring a grid of a given shape.
+__global__ void probe_empty_kernel(uint32_t* out) {
+  extern __shared__ char dyn_lds[];
+  if (threadIdx.x == 0 && blockIdx.x == 0x7fffffff) out[0] = (uint32_t)(uintptr_t)dyn_lds;
+}
+
 }  // namespace
 }  // namespace gllm
 
@@ -138,5 +146,13 @@ extern "C" int gllm_probe_mfma(int32_t mode, int32_t iters, void* out, void* str
     hipLaunchKernelGGL(probe_mfma_kernel<0>, dim3(1), dim3(64), 0, (hipStream_t)stream, (int)iters, (int64_t*)out);
   else
     hipLaunchKernelGGL(probe_mfma_kernel<1>, dim3(1), dim3(64), 0, (hipStream_t)stream, (int)iters, (int64_t*)out);
+  return (int)hipGetLastError();
+}
+
+// An empty grid of wgs workgroups of threads threads (<= 1024) with lds bytes
+// of LDS each (<= 64 KB).
+extern "C" int gllm_probe_empty(int32_t wgs, int32_t threads, int32_t lds, void* out, void* stream) {
+  if (!out || wgs <= 0 || threads <= 0 || threads > 1024 || lds < 0 || lds > 65536) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(probe_empty_kernel, dim3(wgs), dim3(threads), (size_t)lds, (hipStream_t)stream, (uint32_t*)out);
   return (int)hipGetLastError();
 }

@@ -6,7 +6,8 @@
 Loads the timestamp build of the library (the kernels record every
 workgroup's start and end with the 100 MHz ``s_memrealtime`` counter, its
 kind, XCD and keys), runs the benchmark configuration's launch a few times
-and prints, for the last launch: the span from the first start to the last
+over rotating KV pools (``--copies``, as bench.py) and prints, for the last
+launch: the span from the first start to the last
 end, the start spread, durations and end times by kind, the end time of each
 XCD, and how many workgroups of each kind are running every 25 µs.  The
 launch is timed with HIP events too, so the time outside the workgroups'
@@ -32,6 +33,9 @@ def main() -> None:
     ap.add_argument("--split", type=int, default=0, help="split_tokens of the plan (0: the planner's choice)")
     ap.add_argument("--reps", type=int, default=5)
     ap.add_argument("--save", default="", help="also write the raw records (int64 [n, 4]) to this .npy file")
+    ap.add_argument("--copies", type=int, default=4,
+                    help="KV pools the launches rotate through (as bench.py), so a batch smaller than the "
+                         "256 MB Infinity Cache is still read from HBM")
     args = ap.parse_args()
     if not os.path.exists(build.TS_LIB):
         raise SystemExit(f"{build.TS_LIB} not found: run `python -m gllm_amd.build --timestamps` first")
@@ -42,14 +46,20 @@ def main() -> None:
 
     dev = torch.device("cuda", 0)
     b = getattr(workloads, f"config_{args.config}")()
-    x = workloads.materialize(b, dev, values_on_device=True)
+    xs = []
+    for i in range(max(1, args.copies)):
+        c = workloads.PagedBatch(**{k: getattr(b, k) for k in (
+            "name", "ctx_lens", "q_lens", "num_q_heads", "num_kv_heads", "head_dim", "block_size",
+            "num_blocks", "dtype", "rope_theta", "kv_dtype")})
+        xs.append(workloads.materialize(c, dev, values_on_device=True, seed=2 + i))
     plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=b.num_q_heads, num_kv_heads=b.num_kv_heads,
                                head_dim=b.head_dim, block_size=b.block_size, dtype=b.dtype, device=dev,
                                split_tokens=args.split)
-    out = torch.empty_like(x.q)
-    rope = (x.cos, x.sin, "position") if args.config == "c" else None
+    out = torch.empty_like(xs[0].q)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    for _ in range(max(1, args.reps)):
+    for r in range(max(1, args.reps)):
+        x = xs[r % len(xs)]
+        rope = (x.cos, x.sin, "position") if args.config == "c" else None
         e0.record()
         paged.paged_attention(plan, x.q, x.k_cache, x.v_cache, x.block_table, out=out, rope=rope)
         e1.record()
