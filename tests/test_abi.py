@@ -42,6 +42,17 @@ def test_probe_library_loads():
     assert lib.gllm_probe_read(1, 12345, 8, 1, None) != 0          # not a multiple of wgs x 32 KB
     assert lib.gllm_probe_lds_dma(1, 3 << 20, 8, 16, 1, None) != 0  # window not a power of two
     assert lib.gllm_probe_mfma(2, 16, 1, None) != 0                 # unknown mode
+    lib.gllm_probe_empty.argtypes = [i32, i32, i32, p, p]
+    assert lib.gllm_probe_empty(8, 2048, 0, 1, None) != 0          # more than 1024 threads
+
+
+def test_timeline_tool_help():
+    """gllm_amd.timeline parses its arguments without a GPU (it needs the
+    timestamp build and a GPU only to run)."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, "-m", "gllm_amd.timeline", "--help"], capture_output=True, text=True, cwd=ROOT)
+    assert r.returncode == 0 and "--copies" in r.stdout
 
 
 def test_planner_host_logic():
