@@ -47,14 +47,19 @@ def test_fp8_prefill_parity(Hq, Hkv, D):
     assert_close_bf16(out, oracle_paged(b), "fp8 prefill")
 
 
-def test_fp8_mixed_parity():
-    print("fp8 mixed", flush=True)
-    b = _fp8(make_batch([700, 0, 250, 40, 1500], [1, 90, 1, 33, 1], 32, 8, 128))
-    plan = _plan(b)
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("split", [0, paged.BALANCED])
+def test_fp8_mixed_parity(D, split):
+    """Mixed batch over an fp8 pool: the item plan and the page-balanced
+    decode share with prefill items."""
+    print(f"fp8 mixed D={D} split={split}", flush=True)
+    b = _fp8(make_batch([700, 0, 250, 40, 1500], [1, 90, 1, 33, 1], 32, 8, D))
+    plan = _plan(b, split_tokens=split)
     assert plan.info["decode_seqs"] == 3 and plan.info["prefill_seqs"] == 2
+    assert (plan.info["decode_segments"] > 0) == (split == paged.BALANCED)
     out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
     torch.cuda.synchronize()
-    assert_close_bf16(out, oracle_paged(b), "fp8 mixed")
+    assert_close_bf16(out, oracle_paged(b), f"fp8 mixed D={D} split={split}")
 
 
 def test_fp8_cache_under_fp32_model():
