@@ -797,7 +797,8 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
       // items spread through all the decode items, 464 / 463 with them in the
       // first 40% / 30%, 485 with all of them first and 512 with them last.
       // Decode-only item plans: snake order, the direction alternating every
-      // `cus` items, so each CU pairs long work with short.
+      // `cus` items, so each CU pairs long work with short (decode_8b: 396
+      // against 406 µs in plain longest-first order, same box).
       size_t di = 0;
       for (size_t i = 0; i < pf.size(); ++i) {
         const size_t upto = i * dc.size() / (2 * pf.size());
