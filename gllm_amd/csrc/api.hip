@@ -797,8 +797,10 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
       // items spread through all the decode items, 464 / 463 with them in the
       // first 40% / 30%, 485 with all of them first and 512 with them last.
       // Decode-only item plans: snake order, the direction alternating every
-      // `cus` items, so each CU pairs long work with short (decode_8b: 396
-      // against 406 µs in plain longest-first order, same box).
+      // cus / 8 items, so long and short work interleave as slots free up
+      // (decode_8b on one box: 390.5 µs against 397.5 with the direction
+      // alternating every cus items, 402 / 413 every 1.5 / 2 cus, 390.7
+      // every cus / 4, 406 in plain longest-first order).
       size_t di = 0;
       for (size_t i = 0; i < pf.size(); ++i) {
         const size_t upto = i * dc.size() / (2 * pf.size());
@@ -806,9 +808,11 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
         all.push_back(pf[i]);
       }
       while (di < dc.size()) all.push_back(dc[di++]);
-      if (pf.empty())
-        for (size_t c0 = ncu, chunk = 1; c0 < all.size(); c0 += ncu, ++chunk)
-          if (chunk & 1) std::reverse(all.begin() + c0, all.begin() + std::min(all.size(), c0 + ncu));
+      if (pf.empty()) {
+        const size_t per = std::max<size_t>(8, ncu / 8);
+        for (size_t c0 = per, chunk = 1; c0 < all.size(); c0 += per, ++chunk)
+          if (chunk & 1) std::reverse(all.begin() + c0, all.begin() + std::min(all.size(), c0 + per));
+      }
     }
     p->items.reserve(all.size());
     for (auto& k : all) p->items.push_back(k.it);
