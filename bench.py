@@ -318,81 +318,10 @@ def progress(what: str) -> None:
     print(f"[bench] {what}", file=sys.stderr, flush=True)
 
 
-def _probe_lib():
-    """libgllm_probe.so (built beside the attention library by gllm_amd.build):
-    the read-stream and L2 -> LDS copy probes of the box ceilings."""
-    import ctypes
-    from gllm_amd import build as gb
-    lib = ctypes.CDLL(gb.PROBE_LIB)
-    p, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
-    lib.gllm_probe_read.argtypes = [p, i64, i32, p, p]
-    lib.gllm_probe_lds_dma.argtypes = [p, i64, i32, i32, p, p]
-    lib.gllm_probe_mfma.argtypes = [i32, i32, p, p]
-    lib.gllm_probe_empty.argtypes = [i32, i32, i32, p, p]
-    return lib
-
-
-def _probe_ceilings(lib, dev, warmup, reps):
-    """The probes of libgllm_probe.so: an 8 GiB read stream (4 workgroups per
-    CU), a 2 MiB L2-resident window copied into LDS rings (2 per CU), and one
-    wave's MFMA issue / MFMA + VALU overlap cycles and clock."""
-    cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    sink = torch.zeros(8 * cus, dtype=torch.int32, device=dev)
-    rbytes = 8 << 30
-    wgs = 4 * cus
-    rbytes -= rbytes % (wgs * 32768)
-    buf = torch.empty(rbytes, dtype=torch.uint8, device=dev).fill_(1)
-
-    def read_once():
-        rc = lib.gllm_probe_read(buf.data_ptr(), rbytes, wgs, sink.data_ptr(), _lib.stream_ptr(dev))
-        if rc:
-            raise RuntimeError(f"gllm_probe_read: hip error {rc}")
-    per, _ = graph_reps([read_once], warmup, max(5, reps // 2), 1)
-    read_ms = statistics.median(per)
-    del buf
-    window, iters, lwgs = 2 << 20, 2048, 2 * cus
-    win = torch.empty(window, dtype=torch.uint8, device=dev).fill_(1)
-
-    def lds_once():
-        rc = lib.gllm_probe_lds_dma(win.data_ptr(), window, lwgs, iters, sink.data_ptr(), _lib.stream_ptr(dev))
-        if rc:
-            raise RuntimeError(f"gllm_probe_lds_dma: hip error {rc}")
-    per, _ = graph_reps([lds_once], warmup, max(5, reps // 2), 1)
-    lds_ms = statistics.median(per)
-    del win, sink
-    mf = torch.zeros(2, 4, dtype=torch.int64, device=dev)
-    for mode in (0, 1):
-        for _ in range(2):   # the second run is the one kept (clocks settled)
-            rc = lib.gllm_probe_mfma(mode, 4096, mf[mode].data_ptr(), _lib.stream_ptr(dev))
-            if rc:
-                raise RuntimeError(f"gllm_probe_mfma: hip error {rc}")
-            torch.cuda.synchronize()
-    mf = mf.cpu().tolist()
-    # launch cost of config (b)'s grid shape (512 workgroups of 512 threads,
-    # 33 KB of LDS each), doing nothing: per node of a 32-node graph
-    dummy = torch.zeros(1, dtype=torch.int32, device=dev)
-
-    def empty_once():
-        rc = lib.gllm_probe_empty(512, 512, 33 * 1024, dummy.data_ptr(), _lib.stream_ptr(dev))
-        if rc:
-            raise RuntimeError(f"gllm_probe_empty: hip error {rc}")
-    per, _ = graph_reps([empty_once], warmup, max(5, reps // 2), 32)
-    empty_us = statistics.median(per) * 1e3
-    torch.cuda.empty_cache()
-    return {"read_8gib_gbs": rbytes / (read_ms * 1e-3) / 1e9,
-            "read_frac_of_hbm_peak": rbytes / (read_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-            "l2_to_lds_2mib_tbs": lwgs * iters * 4096 / (lds_ms * 1e-3) / 1e12,
-            "mfma32x32x16_bf16_cycles_per_8": mf[0][0], "mfma_8_plus_64_fma_cycles": mf[1][0],
-            "one_wave_shader_clock_ghz": mf[0][0] * mf[0][3] / (mf[0][1] * 10.0),
-            "empty_512x512_graph_us": empty_us}
-
-
 def bench_box_ceilings(dev, warmup, reps):
     """What this box reaches on plain patterns, as context for the roofline
     fractions (not the peaks they are priced against): a device copy of 2 GiB
-    (torch's copy kernel; bytes read + written), the probes of
-    ``_probe_ceilings`` (skipped with a note if libgllm_probe.so is absent),
-    the time per graph node of a one-element kernel (the launch floor of a
+    (torch's copy kernel; bytes read + written), the time per graph node of a one-element kernel (the launch floor of a
     graph-replayed step) and a bf16 8192^3 GEMM (torch.mm -> hipBLASLt)."""
     src = torch.empty(1 << 30, dtype=torch.bfloat16, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
@@ -402,13 +331,6 @@ def bench_box_ceilings(dev, warmup, reps):
     cb = 2 * (2 << 30)
     out = {"copy_2gib_gbs": cb / (copy_ms * 1e-3) / 1e9,
            "copy_frac_of_hbm_peak": cb / (copy_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
-    try:
-        lib = _probe_lib()
-    except OSError as e:   # context only: the metric does not depend on it
-        print(f"[bench] probe library not loaded ({e}); copy / GEMM references only", file=sys.stderr)
-        lib = None
-    if lib is not None:
-        out.update(_probe_ceilings(lib, dev, warmup, reps))
     # launch floor: a one-element kernel per graph node, 32 nodes per graph
     one = torch.zeros(1, device=dev)
     per, _ = graph_reps([lambda: one.add_(1.0)], warmup, max(5, reps // 2), 32)

@@ -15,6 +15,7 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -38,12 +39,13 @@ class AttentionMetadata:
     block_size: int | None = None
 
 
-def _block_size(meta, ql: list[int], sl: list[int]) -> int:
+def _block_size(meta, ql: list[int], sl: list[int], hint: int | None = None) -> int:
     """The pool's block size, checked against the metadata itself: the first
     and the last real query row of the longest sequence must sit at
     ``block_table[i][p // bs] * bs + p % bs`` (``llm.py:245-247,277``).  A
-    given ``block_size`` that disagrees raises; without one, the unique size
-    in 1..1024 that reproduces both slots is taken."""
+    given ``block_size`` that disagrees raises; without one, ``hint`` (the
+    size this caller derived before) is taken if it fits, else the unique
+    size in 1..1024 that reproduces both slots (one vectorised pass)."""
     i = max(range(len(sl)), key=lambda j: sl[j])
     rows = [0, ql[i] - 1]
     ctx = sl[i] - ql[i]
@@ -59,7 +61,16 @@ def _block_size(meta, ql: list[int], sl: list[int]) -> int:
         if not fits(int(given)):
             raise ValueError(f"block_size {given} does not match the slot mapping (sequence {i}, rows {rows})")
         return int(given)
-    cands = [bs for bs in range(1, 1025) if fits(bs)]
+    if hint is not None and fits(hint):
+        return hint
+    sizes = np.arange(1, 1025, dtype=np.int64)
+    table = np.asarray(bt + [0], dtype=np.int64)
+    ok = np.ones_like(sizes, dtype=bool)
+    for p, s in zip(pos, slots):
+        blk = p // sizes
+        inside = blk < len(bt)
+        ok &= inside & (table[np.where(inside, blk, len(bt))] * sizes + p % sizes == s)
+    cands = sizes[ok].tolist()
     if len(cands) != 1:
         raise ValueError(f"cannot derive the block size from the slot mapping ({len(cands)} candidates); "
                          "set AttentionMetadata.block_size")
@@ -67,17 +78,18 @@ def _block_size(meta, ql: list[int], sl: list[int]) -> int:
 
 
 def plan_for(meta, *, num_q_heads: int, num_kv_heads: int, head_dim: int,
-             dtype: torch.dtype, device) -> paged.AttentionPlan:
+             dtype: torch.dtype, device, block_size_hint: int | None = None) -> paged.AttentionPlan:
     """The batch plan, built once per metadata object (one engine step) and
     reused by every layer.  Reads the lengths back once, like the reference's
     own ``.tolist()`` / ``.item()`` calls in ``llm.py:166,176``.  ``meta`` is
     this module's :class:`AttentionMetadata` or the reference's (no
-    ``block_size``: derived from the slot mapping)."""
+    ``block_size``: derived from the slot mapping, or ``block_size_hint``
+    checked against it)."""
     plan = getattr(meta, "_gllm_plan", None)
     if plan is None:
         ql = meta.query_lens.tolist()
         sl = meta.seq_lens.tolist()
-        bs = _block_size(meta, ql, sl)
+        bs = _block_size(meta, ql, sl, block_size_hint)
         plan = paged.AttentionPlan(ql, sl, num_q_heads=num_q_heads, num_kv_heads=num_kv_heads,
                                    head_dim=head_dim, block_size=bs, dtype=dtype,
                                    device=device, q_seq_stride=meta.query_slot_mapping.shape[1])
@@ -106,6 +118,7 @@ class Attention:
         self.W_k = safetensors[f"{pre}.k_proj.weight"].to(dtype=dt)
         self.W_v = safetensors[f"{pre}.v_proj.weight"].to(dtype=dt)
         self.W_o = safetensors[f"{pre}.o_proj.weight"].to(dtype=dt)
+        self._block_size = None          # the pool's block size, once derived from a slot mapping
 
     def apply_rope(self, q: torch.Tensor, k: torch.Tensor, cos_pos: torch.Tensor, sin_pos: torch.Tensor):
         """``attention.py:76-119`` (bit-identical rounding) on the HIP kernel."""
@@ -129,6 +142,8 @@ class Attention:
         paged.rope_kv_write(k, v, cos_pos, sin_pos, k_cache, v_cache, meta.query_slot_mapping,
                             query_lens=meta.query_lens)
         plan = plan_for(meta, num_q_heads=self.num_q_heads, num_kv_heads=self.num_kv_heads,
-                        head_dim=self.head_dim, dtype=q.dtype, device=q.device)
+                        head_dim=self.head_dim, dtype=q.dtype, device=q.device,
+                        block_size_hint=self._block_size)
+        self._block_size = plan.block_size
         return paged.paged_attention(plan, q, k_cache, v_cache, meta.block_table,
                                      rope=(cos_pos, sin_pos, "row"))

@@ -1,11 +1,9 @@
 """Builds libgllm_attn.so (gfx950) in-tree with hipcc.
 
     python -m gllm_amd.build                # or gllm_amd.build.build()
-    python -m gllm_amd.build --timestamps   # libgllm_attn_ts.so, for gllm_amd.timeline
 
 Each .hip unit is compiled to an object in parallel, then linked into
-``gllm_amd/lib/libgllm_attn.so`` (the memory-path probes of bench.py's box
-ceilings into ``gllm_amd/lib/libgllm_probe.so``).  Units whose arithmetic must round like the
+``gllm_amd/lib/libgllm_attn.so``.  Units whose arithmetic must round like the
 reference's torch ops are compiled with ``-ffp-contract=off``.
 """
 from __future__ import annotations
@@ -24,9 +22,6 @@ ARCH = "gfx950"
 
 SOURCES = ["api.hip", "rope_kv_write.hip", "paged_attention.hip", "attention_f32.hip", "metadata.hip",
            "qkv_proj.hip"]
-# memory-path probes behind bench.py's box ceilings (own library, not the attention path)
-PROBE_SOURCES = ["probe.hip"]
-PROBE_LIB = os.path.join(LIBDIR, "libgllm_probe.so")
 NO_CONTRACT = {"rope_kv_write.hip", "attention_f32.hip", "qkv_proj.hip"}
 # MFMA accumulators stay in VGPRs (no per-tile AGPR<->VGPR copies)
 EXTRA = {"paged_attention.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"]}
@@ -38,12 +33,9 @@ COMMON = [
 ]
 
 
-TS_LIB = os.path.join(LIBDIR, "libgllm_attn_ts.so")   # per-workgroup timestamp build (gllm_amd.timeline)
-
-
-def _compile(src: str, defines=()) -> str:
-    obj = os.path.join(LIBDIR, src.replace(".hip", "_ts.o" if defines else ".o"))
-    cmd = [HIPCC, *COMMON, *[f"-D{d}" for d in defines], "-c", os.path.join(CSRC, src), "-o", obj]
+def _compile(src: str) -> str:
+    obj = os.path.join(LIBDIR, src.replace(".hip", ".o"))
+    cmd = [HIPCC, *COMMON, "-c", os.path.join(CSRC, src), "-o", obj]
     if src in NO_CONTRACT:
         cmd.insert(1, "-ffp-contract=off")
     cmd[1:1] = EXTRA.get(src, [])
@@ -67,30 +59,14 @@ def _link(objs, out, extra):
 def build(verbose: bool = False) -> str:
     os.makedirs(LIBDIR, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(4, os.cpu_count() or 1)) as ex:
-        objs = list(ex.map(_compile, SOURCES + PROBE_SOURCES))
+        objs = list(ex.map(_compile, SOURCES))
     # roctx ranges around the entry points
-    _link(objs[:len(SOURCES)], LIB, ["-L/opt/rocm/lib", "-lrocprofiler-sdk-roctx", "-Wl,-rpath,/opt/rocm/lib"])
-    _link(objs[len(SOURCES):], PROBE_LIB, [])
+    _link(objs, LIB, ["-L/opt/rocm/lib", "-lrocprofiler-sdk-roctx", "-Wl,-rpath,/opt/rocm/lib"])
     if verbose:
-        print(f"built {LIB} and {PROBE_LIB}")
+        print(f"built {LIB}")
     return LIB
 
 
-def build_timestamps(verbose: bool = False) -> str:
-    """The attention library with per-workgroup timestamps
-    (-DGLLM_TIMESTAMPS) as libgllm_attn_ts.so, for ``gllm_amd.timeline``."""
-    os.makedirs(LIBDIR, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(4, os.cpu_count() or 1)) as ex:
-        objs = list(ex.map(lambda src: _compile(src, ("GLLM_TIMESTAMPS",)), SOURCES))
-    _link(objs, TS_LIB, ["-L/opt/rocm/lib", "-lrocprofiler-sdk-roctx", "-Wl,-rpath,/opt/rocm/lib"])
-    if verbose:
-        print(f"built {TS_LIB}")
-    return TS_LIB
-
-
 if __name__ == "__main__":
-    if "--timestamps" in sys.argv[1:]:
-        build_timestamps(verbose=True)
-    else:
-        build(verbose=True)
+    build(verbose=True)
     sys.exit(0)

@@ -188,6 +188,14 @@ __device__ __forceinline__ float sum_xor32(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// c + lo + hi of two packed bf16 values (one v_dot2c_f32_bf16 against 1.0):
+// softmax row sums taken over the bf16-rounded p that the P V MFMA
+// multiplies, so numerator and denominator weigh every key alike.
+__device__ __forceinline__ float add_bf16x2(uint32_t w, float c) {
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, c, false);
+}
+
 // Division by the KV block size (any size >= 1): floor(p / bs) for
 // 0 <= p < 2^31 is umulhi(2p, magic) >> shift with k = ceil(log2 bs),
 // magic = ceil(2^(31+k) / bs), shift = k.  Exact: with e = magic bs - 2^(31+k)

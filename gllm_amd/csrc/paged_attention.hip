@@ -25,37 +25,6 @@
 
 namespace gllm {
 
-// Per-workgroup timeline, only in the timestamp build (-DGLLM_TIMESTAMPS,
-// `python -m gllm_amd.build --timestamps`, read by gllm_amd/timeline.py):
-// thread 0 of each of the first 32768 workgroups of a launch records its
-// start and end (s_memrealtime, 100 MHz), its kind (0 decode item, 1 prefill
-// item, 2 decode segments) with the XCD it ran on, and its keys.  The record
-// is written when the kernel body returns, on every path.
-#ifdef GLLM_TIMESTAMPS
-__device__ long long gllm_ts_buf[4 << 15];
-struct WgStamp {
-  long long t0;
-  int kind = 0, keys = 0;
-  __device__ WgStamp() : t0(__builtin_amdgcn_s_memrealtime()) {}
-  __device__ ~WgStamp() {
-    if (threadIdx.x == 0 && blockIdx.x < (1u << 15)) {
-      unsigned x;
-      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
-      long long* d = gllm_ts_buf + 4 * (int64_t)blockIdx.x;
-      d[0] = t0;
-      d[1] = __builtin_amdgcn_s_memrealtime();
-      d[2] = kind | (long long)((x & 15) << 8);
-      d[3] = keys;
-    }
-  }
-};
-#define GLLM_WG_STAMP(name) WgStamp name
-#define GLLM_WG_STAMP_SET(name, k, n) (name.kind = (k), name.keys = (n))
-#else
-#define GLLM_WG_STAMP(name)
-#define GLLM_WG_STAMP_SET(name, k, n) ((void)0)
-#endif
-
 // Rotate-half RoPE on 8 pairs, each op rounded to bf16 like the reference's
 // torch ops (gllm/model/layers/attention.py:105-118).
 __device__ __forceinline__ void rope8_bf16(float* x1, float* x2, const float* c, const float* s) {
@@ -309,8 +278,8 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
     const float mu = m == kNegInf ? 0.f : m;
 #pragma unroll
     for (int j = 0; j < 4; ++j) p[j] = fast_exp2(p[j] - mu);
-    lsum += (p[0] + p[1]) + (p[2] + p[3]);
     const u32x2 pb = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
+    lsum = add_bf16x2(pb[1], add_bf16x2(pb[0], lsum));   // the rounded p the MFMA sees
     const char* vrow = ldsV + (4 * grp + (n >> 2)) * RB + 4 * (n & 3) * 2;
 #pragma unroll
     for (int d = 0; d < ND; ++d) acc[d] = mfma16k16(lds_read_tr16(vrow + 32 * d), pb, acc[d]);
@@ -761,7 +730,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 
   const float sl2 = a.scale * kLog2e;
   float m = kNegInf, lsum = 0.f;
-  float sbase = 0.f;             // dense mode: value the tile's S accumulators start from
+  float sbase = 0.f;             // dense mode: -(the running max) at the tile's start
   f32x16 o[NO];
 #pragma unroll
   for (int db = 0; db < NO; ++db)
@@ -770,30 +739,33 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 
   // Softmax of one 32-key half, in pieces that the tile loop interleaves
   // with MFMAs: lane holds raw scores S[key k0 + 8(j/4) + 4h + j%4][row n].
-  // Q is pre-scaled by scale * log2(e), so scores come out in log2 units.
+  // Q enters the MFMA as the exact bf16 value (rotated like apply_rope); the
+  // raw fp32 dot products are scaled by scale * log2(e) in fp32, so scores in
+  // log2 units carry one fp32 rounding, like the reference's q @ k^T / sqrt(D)
+  // (rounding q * scale to bf16 instead would move a score s by up to
+  // |s| 2^-9, which at large logits reweights the keys visibly).
   //
-  // Paged (causal) mode: each row keeps a reference r and p = 2^(s - r).  The
+  // Paged (causal) mode: each row keeps a reference r and p = 2^(s - r), the
+  // scale and the reference applied together by one FMA per score.  The
   // first half-tile of the row (keys 0..31; key 0 is visible to every row)
   // sets r = 0 when its max m1 lies in [-T, T] and r = m1 otherwise, so every
   // row holds some p >= 2^-T and later tiny p lose nothing.  After that S
-  // accumulates from zero and, while r = 0, p = 2^s directly: no S
-  // initialisation, no running max, no subtraction per score.  The only check
-  // is one compare of each lane's partial sum against 2^T: a lane over it
-  // (some p > 2^T) sends the wave into a rare fix-up that recomputes the
+  // accumulates from zero: no S initialisation, no running max.  The only
+  // check is one compare of each lane's partial sum against 2^T: a lane over
+  // it (some p > 2^T) sends the wave into a rare fix-up that recomputes the
   // half's S from LDS, moves the reference of every row whose max passed T up
   // to that max (O and l rescaled by 2^-max, exactly) and recomputes p.  With
   // T = 64, p <= 2^64 keeps l and O far from fp32 overflow.  Numerator and
   // denominator share r, so the result is the exact softmax.
   //
   // Dense (arbitrary bias) mode: lazy running max (the max only moves when a
-  // row's max exceeds it by more than 8, so p <= 2^8); the S accumulators
-  // start at -m, so the MFMA yields s - m directly (a subtract of the max's
-  // move otherwise, rare).
+  // row's max exceeds it by more than 8, so p <= 2^8); scale, bias and the
+  // tile's starting offset -m enter one FMA per score, so the exponent is
+  // s - m directly (a subtract of the max's move otherwise, rare).
   constexpr bool kFast = !DENSE;
   constexpr float kT = 64.f;
   constexpr float kTwoT = 18446744073709551616.f;   // 2^64
   float rref = 0.f;              // paged mode: the row's reference r (log2 units)
-  bool sub = false;              // paged mode, wave-uniform: some row has r != 0
   struct Soft { float alpha, dlt, psum; };
   auto row_max = [&](const f32x16& s) {
     float tmax = kNegInf;
@@ -811,19 +783,17 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 #pragma unroll
     for (int j = 0; j < 16; ++j) s[j] = 8 * (j >> 2) + (j & 3) > lim ? kNegInf : s[j];
   };
-  // paged mode, piece 0: the reference's subtraction (rare), the causal mask,
-  // and on the row's first half-tile the choice of r
+  // paged mode, piece 0: scale and reference (one FMA), the causal mask, and
+  // on the row's first half-tile the choice of r
   auto fs_prep = [&](f32x16& s, int k0, bool mask, bool first) {
-    if (sub) {
+    const float nr = -rref;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) s[j] -= rref;
-    }
+    for (int j = 0; j < 16; ++j) s[j] = __builtin_fmaf(s[j], sl2, nr);
     if (mask) apply_mask(s, k0);
     if (first) {
       const float m1 = row_max(s);
       rref = (m1 >= -kT && m1 <= kT) || m1 == kNegInf ? 0.f : m1;
-      sub = __builtin_amdgcn_ballot_w64(rref != 0.f) != 0;
-      if (sub) {
+      if (__builtin_amdgcn_ballot_w64(rref != 0.f)) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) s[j] -= rref;
       }
@@ -836,7 +806,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
       for (int j = 0; j < 16; ++j) {   // bias in natural-log units: to log2 units like the scaled scores
         const int key = k0 + 8 * (j >> 2) + 4 * h + (j & 3);
         const float bv = key < T ? (float)bp[key] : kNegInf;
-        s[j] = __builtin_fmaf(bv, kLog2e, s[j]);
+        s[j] = __builtin_fmaf(s[j], sl2, __builtin_fmaf(bv, kLog2e, sbase));
       }
     } else if (mask) {
       apply_mask(s, k0);
@@ -856,11 +826,16 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 #pragma unroll
     for (int j = j0; j < j0 + 4; ++j) s[j] = fast_exp2(s[j]);
   };
-  auto sm_sum = [&](const f32x16& s, Soft& q) {
-    float ps4[4];
+  // row sum of the half's bf16-rounded p (the values the P V MFMA takes)
+  auto sm_sum = [&](const bf16x8* pb, Soft& q) {
+    const u32x4 w0 = __builtin_bit_cast(u32x4, pb[0]), w1 = __builtin_bit_cast(u32x4, pb[1]);
+    float a0 = add_bf16x2(w0[0], 0.f), a1 = add_bf16x2(w1[0], 0.f);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) ps4[e] = (s[e] + s[e + 4]) + (s[e + 8] + s[e + 12]);
-    q.psum = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
+    for (int e = 1; e < 4; ++e) {
+      a0 = add_bf16x2(w0[e], a0);
+      a1 = add_bf16x2(w1[e], a1);
+    }
+    q.psum = a0 + a1;
     if (!kFast) lsum = __builtin_fmaf(lsum, q.alpha, q.psum);
   };
   auto sm_cvt = [&](const f32x16& s, bf16x8* pb) {
@@ -873,15 +848,15 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
     pb[1] = to_bf16x8(pv);
   };
   // Logical softmax piece p (0..7) of a half: max (dense) or prep (paged),
-  // 4 x exp, sum, convert.
+  // 4 x exp, convert, sum.
   auto sm_piece = [&](int p, f32x16& s, int k0, bool mask, Soft& q, bf16x8* pb, bool first) {
     if (p == 0) {
       if (kFast) fs_prep(s, k0, mask, first);
       else sm_max(s, k0, mask, q);
     }
     else if (p <= 4) sm_exp(s, 4 * (p - 1));
-    else if (p == 5) sm_sum(s, q);
-    else if (p == 6) sm_cvt(s, pb);
+    else if (p == 5) sm_cvt(s, pb);
+    else if (p == 6) sm_sum(pb, q);
   };
   // After a half's pieces.  Dense: the rare O rescale of the lazy max
   // (q.psum >= 0 always; testing it keeps the half's exponentials ahead of
@@ -901,10 +876,9 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 #pragma unroll
       for (int kk = 0; kk < NQ; ++kk)
         t = mfma32(as_bf16x8(*reinterpret_cast<const u32x4*>(st + 32 * kb * RW + koff[kk])), qB[kk], t);
-      if (sub) {
+      const float nr = -rref;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) t[j] -= rref;
-      }
+      for (int j = 0; j < 16; ++j) t[j] = __builtin_fmaf(t[j], sl2, nr);
       if (mask) apply_mask(t, k0);
       const float tmax = row_max(t);
       const float d = tmax > kT ? tmax : 0.f;          // rows whose p passed 2^T move up to their max
@@ -913,10 +887,19 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
       for (int db = 0; db < NO; ++db) o[db] *= alpha;
       lsum *= alpha;
       rref += d;
-      sub = __builtin_amdgcn_ballot_w64(rref != 0.f) != 0;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) t[j] = fast_exp2(t[j] - d);
-      sm_sum(t, q);
+      for (int j = 0; j < 16; j += 2) {
+        float e0 = fast_exp2(t[j] - d), e1 = fast_exp2(t[j + 1] - d);
+        round2_bf16(e0, e1);                    // the values the P V MFMA takes
+        t[j] = e0;
+        t[j + 1] = e1;
+      }
+      // summed in fp32 here (a sum over the packed operands on this rare path
+      // costs the common path ~30 VGPRs in the compiler's allocation)
+      float ps4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ps4[e] = (t[e] + t[e + 4]) + (t[e + 8] + t[e + 12]);
+      q.psum = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
       sm_cvt(t, pb);
     }
     lsum += q.psum;
@@ -950,14 +933,9 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
     u32x4 ka[2][NQ];
 #pragma unroll
     for (int kk = 0; kk < NQ; ++kk) ka[0][kk] = *reinterpret_cast<const u32x4*>(st + koff[kk]);
-    if (kFast) {
-      s0 = f32x16{};
-      s1 = f32x16{};
-    } else {
-      sbase = m == kNegInf ? 0.f : -m;     // both halves start from the max before this tile
-#pragma unroll
-      for (int j = 0; j < 16; ++j) s0[j] = sbase, s1[j] = sbase;
-    }
+    s0 = f32x16{};
+    s1 = f32x16{};
+    if (!kFast) sbase = m == kNegInf ? 0.f : -m;   // both halves start from the max before this tile
     // K of half 1 is read between the MFMAs of half 0: the eight waves' reads
     // after a barrier do not all hit LDS at once, and fewer registers are live
 #pragma unroll
@@ -1083,11 +1061,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
       }
     }
 #pragma unroll
-    for (int kk = 0; kk < NQ; ++kk) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) x[kk][i] *= sl2;     // scores come out in log2 units
-      qB[kk] = to_bf16x8(x[kk]);
-    }
+    for (int kk = 0; kk < NQ; ++kk) qB[kk] = to_bf16x8(x[kk]);   // exact: q and its rotation are bf16
   }
   if (!DENSE) __syncthreads();  // block ids in LDS visible
   if (TPB < ntiles) dma_bids(TPB * BN, nbid);
@@ -1166,9 +1140,7 @@ __device__ __forceinline__ int xcd_item(int b, int n) {
 template <int D, bool PF, bool DC, int HW, int KW, bool KV8>
 __global__ void __launch_bounds__(64 * HW * KW) paged_attn_bf16_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[MixedLds<D, PF, DC, HW * KW>::kBytes];
-  GLLM_WG_STAMP(stamp);
   const WorkItem it = a.items[xcd_item<!PF && KV8 && HW * D < 128>(blockIdx.x, a.n_items)];
-  GLLM_WG_STAMP_SET(stamp, (it.kind_b & 0xff) == kItemPrefill ? 1 : 0, it.ctx_len + it.q_len);
   if (PF && (!DC || (it.kind_b & 0xff) == kItemPrefill)) {
     if constexpr (HW * KW == kWaves)
       prefill_wg<D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
@@ -1184,9 +1156,7 @@ __global__ void __launch_bounds__(64 * HW * KW) __attribute__((amdgpu_waves_per_
 decode_balanced_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[DecodeCfg<D, HW * KW>::kLdsBytes];
   __shared__ int ticket;
-  GLLM_WG_STAMP(stamp);
   const int s0 = a.seg_ptr[blockIdx.x], s1 = a.seg_ptr[blockIdx.x + 1];
-  GLLM_WG_STAMP_SET(stamp, 2, s1 - s0);
   for (int s = s0; s < s1; ++s) {
     if (s > s0) __syncthreads();
     const DecodeSeg sg = a.segs[s];
@@ -1204,16 +1174,13 @@ template <int D, int HW, bool KV8>
 __global__ void __launch_bounds__(64 * kWaves) mixed_balanced_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[MixedLds<D, true, true, kWaves>::kBytes];
   __shared__ int ticket;
-  GLLM_WG_STAMP(stamp);
   const int b = blockIdx.x;
   if (b >= a.n_seg_wgs) {
     const WorkItem it = a.items[b - a.n_seg_wgs];
-    GLLM_WG_STAMP_SET(stamp, 1, it.ctx_len + it.q_len);
     prefill_wg<D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
     return;
   }
   const int s0 = a.seg_ptr[b], s1 = a.seg_ptr[b + 1];
-  GLLM_WG_STAMP_SET(stamp, 2, s1 - s0);
   for (int s = s0; s < s1; ++s) {
     if (s > s0) __syncthreads();
     const DecodeSeg sg = a.segs[s];
@@ -1228,9 +1195,7 @@ template <int D, bool KV8>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2)))
 prefill_bf16_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[PrefillCfg<D, kPrefillStages>::kLdsBytes];
-  GLLM_WG_STAMP(stamp);
   const WorkItem it = a.items[blockIdx.x];
-  GLLM_WG_STAMP_SET(stamp, 1, it.ctx_len + it.q_len);
   prefill_wg<D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
 }
 
@@ -1352,12 +1317,3 @@ hipError_t launch_fill_zero_i32(int32_t* p, int64_t n, hipStream_t st) {
 }
 
 }  // namespace gllm
-
-#ifdef GLLM_TIMESTAMPS
-// Copies the timeline records of the last instrumented launch (4 int64 per
-// workgroup) to host memory; returns a hipError_t code.
-extern "C" int gllm_debug_timestamps(void* host, size_t bytes) {
-  if (bytes > sizeof(gllm::gllm_ts_buf)) bytes = sizeof(gllm::gllm_ts_buf);
-  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(gllm::gllm_ts_buf), bytes, 0, hipMemcpyDeviceToHost);
-}
-#endif

@@ -28,33 +28,6 @@ def test_library_exports_every_declared_symbol():
     assert lib.gllm_attn_version() == 1
 
 
-def test_probe_library_loads():
-    """bench.py's box-ceiling probes live in their own library
-    (libgllm_probe.so, not the attention boundary): it loads, exports its
-    three entry points and rejects bad arguments without a GPU."""
-    from gllm_amd import build as gb
-    lib = ctypes.CDLL(gb.PROBE_LIB)
-    p, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
-    lib.gllm_probe_read.argtypes = [p, i64, i32, p, p]
-    lib.gllm_probe_lds_dma.argtypes = [p, i64, i32, i32, p, p]
-    lib.gllm_probe_mfma.argtypes = [i32, i32, p, p]
-    assert lib.gllm_probe_read(None, 1 << 20, 8, None, None) != 0
-    assert lib.gllm_probe_read(1, 12345, 8, 1, None) != 0          # not a multiple of wgs x 32 KB
-    assert lib.gllm_probe_lds_dma(1, 3 << 20, 8, 16, 1, None) != 0  # window not a power of two
-    assert lib.gllm_probe_mfma(2, 16, 1, None) != 0                 # unknown mode
-    lib.gllm_probe_empty.argtypes = [i32, i32, i32, p, p]
-    assert lib.gllm_probe_empty(8, 2048, 0, 1, None) != 0          # more than 1024 threads
-
-
-def test_timeline_tool_help():
-    """gllm_amd.timeline parses its arguments without a GPU (it needs the
-    timestamp build and a GPU only to run)."""
-    import subprocess
-    import sys
-    r = subprocess.run([sys.executable, "-m", "gllm_amd.timeline", "--help"], capture_output=True, text=True, cwd=ROOT)
-    assert r.returncode == 0 and "--copies" in r.stdout
-
-
 def test_planner_host_logic():
     lib = _lib.load()
     h = ctypes.c_void_p()

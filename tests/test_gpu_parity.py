@@ -2,7 +2,6 @@
 inputs).  Bar: bit-exact for the RoPE/KV-write indexing and values; bf16
 attention outputs within max-abs 2e-2 and mean-abs 2e-3 of the fp32 oracle;
 fp32 outputs within 1e-4."""
-import math
 
 import pytest
 import torch
@@ -163,30 +162,20 @@ def test_prefill_parity(Hq, Hkv, D):
 @pytest.mark.parametrize("D", [64, 128])
 def test_prefill_extreme_scores(D):
     """Scores far outside the softmax fast path's range [-64, 64] (log2
-    units): q scaled up (most half-tiles overflow 2^64 and take the fix-up),
-    and a first half-tile far below every later key (the row's reference
-    starts at that max, later tiles move it up).  With scores this peaked a
-    handful of keys carry each row, so the bf16 rounding of P no longer
-    averages out: max-abs is held to 4e-2 here (mean-abs to the usual 2e-3);
-    a wrong rescale would be off by O(1)."""
+    units), against the unmodified fp32 oracle at the usual bar: q scaled up
+    (most half-tiles overflow 2^64 and take the fix-up), and a first
+    half-tile far below every later key (the row's reference starts at that
+    max, later tiles move it up).  The kernel scales the fp32 scores, so
+    large logits cost no precision; a wrong rescale would be off by O(1)."""
     print(f"prefill extreme scores D={D}", flush=True)
     Hq, Hkv = 32, 8
-    # the kernel rounds q * scale * log2(e) to bf16 once; at these magnitudes
-    # that rounding alone moves scores by ~0.3, so the oracle gets the same
-    # effective q (the softmax logic is what is under test here)
-    sl2 = torch.tensor(1.0 / math.sqrt(D), dtype=torch.float32) * torch.tensor(1.4426950408889634,
-                                                                                  dtype=torch.float32)
-
-    def q_eff(q):
-        return (q.float().cpu() * sl2).to(torch.bfloat16).float() / sl2
-
     b = make_batch([0, 0, 100], [200, 70, 90], Hq, Hkv, D)
     b.q.mul_(30.0)                                          # s ~ N(0, (30 * 1.44)^2): row maxima > 64
     plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=D,
                                block_size=16, dtype=torch.bfloat16, device=DEV)
     out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
     torch.cuda.synchronize()
-    assert_close_bf16(out, oracle_paged(b, q_eff(b.q)), "prefill, scaled q", max_abs=4e-2)
+    assert_close_bf16(out, oracle_paged(b), "prefill, scaled q")
     # every query row = u; keys 0..31 of each sequence = -6 u / |u| * sqrt(D): first half-tile
     # scores ~ -6 sqrt(D) * 1.44 < -64, later keys N(0, 1) scores
     g = torch.Generator().manual_seed(7)
@@ -203,7 +192,41 @@ def test_prefill_extreme_scores(D):
                                block_size=16, dtype=torch.bfloat16, device=DEV)
     out = paged.paged_attention(plan, c.q, c.k_cache, c.v_cache, c.block_table)
     torch.cuda.synchronize()
-    assert_close_bf16(out, oracle_paged(c, q_eff(c.q)), "prefill, very negative first tile", max_abs=4e-2)
+    assert_close_bf16(out, oracle_paged(c), "prefill, very negative first tile")
+
+
+@pytest.mark.parametrize("scale", [10.0, 30.0])
+def test_mixed_extreme_scores(scale):
+    """A mixed launch (decode rows and prefill chunks in one grid) with q
+    scaled up, against the unmodified fp32 oracle: both item kinds scale
+    their fp32 scores."""
+    print(f"mixed extreme scores x{scale}", flush=True)
+    b = make_batch([300, 0, 57, 1000, 5], [1, 120, 64, 1, 1], 32, 8, 128)
+    b.q.mul_(scale)
+    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=32, num_kv_heads=8, head_dim=128,
+                               block_size=16, dtype=torch.bfloat16, device=DEV)
+    out = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table)
+    torch.cuda.synchronize()
+    assert_close_bf16(out, oracle_paged(b), "mixed, scaled q")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_dense_op_extreme_scores(D):
+    """The dense-bias op (reference_attention contract) with logits far
+    beyond N(0,1): q scaled by 30, engine-style causal bias, against the
+    fp32 op on the same bf16 inputs."""
+    print(f"dense extreme scores D={D}", flush=True)
+    g = torch.Generator().manual_seed(70 + D)
+    B, Tq, T, Hq, Hkv = 2, 96, 160, 8, 2
+    q = (torch.randn(B, Tq, Hq, D, generator=g) * 30.0).to(torch.bfloat16)
+    k = torch.randn(B, T, Hkv, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, T, Hkv, D, generator=g).to(torch.bfloat16)
+    bias = torch.zeros(B, Tq, T, dtype=torch.bfloat16)
+    bias[:, :, T - Tq:] = torch.full((Tq, Tq), float("-inf")).triu(1).to(torch.bfloat16)
+    ref = oa.reference_attention(q.float(), k.float(), v.float(), bias.float())
+    out = gllm_amd.reference_attention(q.to(DEV), k.to(DEV), v.to(DEV), bias.to(DEV))
+    torch.cuda.synchronize()
+    assert_close_bf16(out, ref, "dense, scaled q")
 
 
 def test_prefill_rope_in_kernel_matches_prerotated():

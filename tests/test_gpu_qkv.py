@@ -329,3 +329,40 @@ def test_qkv_large_batch_unfused_route(integer, rotate_q):
     rest = torch.ones(ns, dtype=torch.bool)
     rest[slots] = False
     assert bool((kc[rest] == 3.0).all()) and bool((vc[rest] == 3.0).all())
+
+
+@pytest.mark.parametrize("n,hidden,split_k", [(16, 256, True),      # one launch, <= 32 tokens
+                                              (96, 1024, True),     # split-K partials + finish
+                                              (600, 128, False)])   # tile kernel
+@pytest.mark.parametrize("pad", ["q_out", "cache"])
+def test_qkv_unaligned_row_strides(n, hidden, split_k, pad):
+    """Row strides that are not multiples of 4 elements (q_out rows of
+    Hq*D + 2, or cache slots of Hkv*D + 2) take the element-wise store path
+    of every kernel: bit-exact against the oracle on exact data, and the
+    padding elements between rows keep their sentinel."""
+    print(f"qkv unaligned {pad} n={n} hidden={hidden} split_k={split_k}", flush=True)
+    Hq, Hkv, D = 8, 2, 64
+    x, (wq, wk, wv), cos_t, sin_t, pos, slots, ns = _inputs(n, hidden, Hq, Hkv, D, True, 50 + n)
+    cpad = 2 if pad == "cache" else 0
+    qpad = 2 if pad == "q_out" else 0
+    kbuf = torch.full((ns, Hkv * D + cpad), 3.0, dtype=BF, device=DEV)
+    vbuf = kbuf.clone()
+    qbuf = torch.full((n, Hq * D + qpad), 7.0, dtype=BF, device=DEV)
+    kc = kbuf[:, :Hkv * D].view(ns, Hkv, D)
+    vc = vbuf[:, :Hkv * D].view(ns, Hkv, D)
+    q_out = qbuf[:, :Hq * D].view(n, Hq, D)
+    assert kc.stride(0) == Hkv * D + cpad and q_out.reshape(-1, Hq * D).stride(0) == Hq * D + qpad
+    from gllm_amd import _lib
+    wsb = _lib.load().gllm_qkv_workspace_bytes(n, hidden, Hq, Hkv, D, 1)
+    assert (wsb > 0) == (split_k and n > 32)                  # the intended path is the one planned
+    paged.qkv_rope_kv_write(x.to(DEV), wq.to(DEV), wk.to(DEV), wv.to(DEV), cos_t.to(DEV), sin_t.to(DEV), kc, vc,
+                            slots.to(DEV), q_out=q_out, rope_rows=pos.to(DEV), split_k=split_k, unfused_from=None)
+    torch.cuda.synchronize()
+    kr = torch.full((ns, Hkv, D), 3.0, dtype=BF)
+    vr = kr.clone()
+    qr = op.qkv_rope_kv_write(x, wq, wk, wv, cos_t[pos], sin_t[pos], kr, vr, slots, Hkv, D)
+    assert torch.equal(q_out.cpu().view(torch.int16), qr.view(torch.int16))
+    assert torch.equal(kc.cpu().view(torch.int16), kr.view(torch.int16))
+    assert torch.equal(vc.cpu().view(torch.int16), vr.view(torch.int16))
+    assert bool((qbuf[:, Hq * D:] == 7.0).all()) and bool((kbuf[:, Hkv * D:] == 3.0).all())
+    assert bool((vbuf[:, Hkv * D:] == 3.0).all())

@@ -80,3 +80,21 @@ def test_noalloc_rejects_partials_beyond_the_scratch():
     inp = _inputs(n, hidden, Hq, Hkv, D, 3)
     with pytest.raises(NotImplementedError, match="static scratch"):
         _call(lib, True, *inp, Hq, Hkv, D)
+
+
+def test_noalloc_first_call_inside_graph_capture():
+    """The use case of the no-alloc entry point: a caller under HIP graph
+    capture.  In a fresh process (so the scratch address is resolved by a
+    call made inside capture), the captured call replays bit-exact against
+    the workspace entry point three times, with eager no-alloc calls on
+    other data between the replays."""
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    print("qkv noalloc: first call inside graph capture (child process)", flush=True)
+    r = subprocess.run([sys.executable, "-u", os.path.join(here, "noalloc_capture_child.py")],
+                       capture_output=True, text=True, timeout=110)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0, r.stdout[-500:] + r.stderr[-1500:]
+    assert r.stdout.count("bit-exact") == 3
