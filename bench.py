@@ -170,6 +170,30 @@ def bench_paged(b, copies, warmup, reps, inner, dev, split=0, hw=0, eager=True, 
     return res, xs[0], outs[0]
 
 
+def bench_prefill_step(b, x, warmup, reps, dev):
+    """Config (c) as one step: the RoPE + KV write of the batch's new tokens
+    (K rotated and written into its pages) followed by the paged attention
+    launch with q rotated on load, both in one graph step.  Work: the
+    attention flops (MFMA roofline) and the step's compulsory bytes (the
+    write's bytes plus the attention's)."""
+    pos = torch.cat([torch.arange(c, c + q) for c, q in zip(b.ctx_lens, b.q_lens)]).to(dev)
+    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=b.num_q_heads, num_kv_heads=b.num_kv_heads,
+                               head_dim=b.head_dim, block_size=b.block_size, dtype=b.dtype, device=dev)
+    out = torch.empty_like(x.q)
+
+    def step():
+        paged.rope_kv_write(x.k_new, x.v_new, x.cos, x.sin, x.k_cache, x.v_cache, x.slot_mapping, rope_rows=pos)
+        paged.paged_attention(plan, x.q, x.k_cache, x.v_cache, x.block_table, out=out,
+                              rope=(x.cos, x.sin, "position"))
+    per, wall = graph_reps([step], warmup, reps, 4)
+    ms = statistics.median(per)
+    flops = workloads.attention_flops(b)
+    nbytes = workloads.rope_write_bytes(b) + workloads.decode_bytes(b)
+    r = roofline_mfma(flops, ms, "prefill_step_8b")
+    return {"ms_per_step": ms, "launches_per_step": 2, "flops_per_step": flops, "bytes_per_step": nbytes,
+            "hbm_gbs": nbytes / (ms * 1e-3) / 1e9, "roofline": r}
+
+
 def bench_rope_write(b, x, warmup, reps, dev):
     """The fused RoPE + KV write of the batch's new tokens (graph-timed)."""
     pos = torch.cat([torch.arange(c, c + q) for c, q in zip(b.ctx_lens, b.q_lens)]).to(dev)
@@ -381,9 +405,9 @@ def cpu_baseline_per_sequence(x: workloads.PagedBatch, seqs: list[int], unit: st
     batch carries a RoPE table, then GQA expand + softmax attention with the
     0/-inf bias (reference_attention.py:5-51), fp32 torch on every host core.
     The metadata build is outside the timed region (once per engine step);
-    one untimed warm-up call, then one timed pass over ``seqs``.  Work per
-    sequence uses the same formulas as the GPU figure, so ``value`` is
-    directly comparable."""
+    one untimed warm-up pass over ``seqs``, then the median of 3 timed
+    passes.  Work per sequence uses the same formulas as the GPU figure, so
+    ``value`` is directly comparable."""
     from oracle import attention as oa
     from oracle import metadata as om
     from oracle import rope as orope
@@ -415,17 +439,21 @@ def cpu_baseline_per_sequence(x: workloads.PagedBatch, seqs: list[int], unit: st
         v = oa.kv_gather(vc, meta.slot_mapping, torch.float32)
         return oa.reference_attention(qq, k, v, meta.bias)
 
-    run(jobs[min(range(len(jobs)), key=lambda j: jobs[j][3].shape[1] * jobs[j][0].shape[0])])
-    t = time.perf_counter()
-    for job in jobs:
-        run(job)
-    sec = time.perf_counter() - t
+    passes = []
+    for rep in range(4):                       # pass 0 is the warm-up
+        t = time.perf_counter()
+        for job in jobs:
+            run(job)
+        if rep:
+            passes.append(time.perf_counter() - t)
+    sec = statistics.median(passes)
     sub = workloads.PagedBatch("sample", [x.ctx_lens[i] for i in seqs], [x.q_lens[i] for i in seqs],
                                x.num_q_heads, Hkv, D, bs, x.num_blocks, x.dtype, kv_dtype=x.kv_dtype)
     work = workloads.decode_bytes(sub) / 1e9 if unit == "GB/s" else workloads.attention_flops(sub) / 1e12
     return {"value": work / sec, "unit": unit, "cores": cores, "kind": "port",
             "sample": f"{what}: {len(seqs)} of {len(x.q_lens)} sequences, one at a time (B=1), "
-                      f"{sec:.2f} s for {work:.4g} {'GB' if unit == 'GB/s' else 'TFLOP'} of the same "
+                      f"median of 3 timed passes after 1 warm-up pass ({', '.join(f'{v:.2f}' for v in passes)} s) "
+                      f"for {work:.4g} {'GB' if unit == 'GB/s' else 'TFLOP'} of the same "
                       f"formula as the GPU figure; fp32 torch on {cores} threads of {cpu_model()}"}
 
 
@@ -505,6 +533,18 @@ def main():
         d = workloads.config_d()
         head, xd, _ = bench_paged(d, 1, args.warmup, reps, 4, dev, args.split, args.hw)
         head["roofline"] = roofline_hbm(head["bytes_per_launch"], head["ms_per_step"], "mixed_8b")
+        # the chunked-prefill part of (d): its flops over the mixed launch's
+        # time, and the 4 chunks launched alone (prefill items only)
+        dch = workloads.PagedBatch("mixed_8b_chunks", d.ctx_lens[256:], d.q_lens[256:], d.num_q_heads,
+                                   d.num_kv_heads, d.head_dim, d.block_size, d.num_blocks, d.dtype,
+                                   rope_theta=d.rope_theta)
+        cf = workloads.attention_flops(dch)
+        rc, _, _ = bench_paged(dch, 2, args.warmup, reps, 4, dev, eager=False)
+        head["chunk_part"] = {
+            "flops": cf, "share_of_launch_flops": cf / head["flops_per_launch"],
+            "roofline_over_mixed_launch": roofline_mfma(cf, head["ms_per_step"], "none"),
+            "alone": {"ms_per_step": rc["ms_per_step"], "work_items": rc["work_items"],
+                      "roofline": roofline_mfma(cf, rc["ms_per_step"], "mixed_8b_chunks")}}
         extra["mixed_8b"] = head
         extra["metadata_mixed_8b"] = bench_metadata(xd, args.warmup, reps, dev, False)
         if cpu:
@@ -527,6 +567,7 @@ def main():
         r, xc, _ = bench_paged(c, 2, args.warmup, reps, 4, dev, eager=False, rope=True)
         r["roofline"] = roofline_mfma(r["flops_per_launch"], r["ms_per_step"], "prefill_8b")
         r["rope_kv_write"] = bench_rope_write(c, xc, args.warmup, reps, dev)
+        r["step"] = bench_prefill_step(c, xc, args.warmup, reps, dev)
         if cpu:
             r["cpu_baseline"] = cpu_baseline_per_sequence(xc, list(range(len(c.q_lens))), "TFLOP/s",
                                                           "all of config (c)")

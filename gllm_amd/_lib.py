@@ -15,7 +15,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libgllm_attn.so")
 
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
-DTYPE_F32, DTYPE_BF16, DTYPE_FP8_E4M3 = 0, 1, 2
+DTYPE_F32, DTYPE_BF16, DTYPE_FP8_E4M3, DTYPE_F16 = 0, 1, 2, 3
 ROPE_NONE, ROPE_BY_POSITION, ROPE_BY_ROW = 0, 1, 2
 
 _p = ctypes.c_void_p
@@ -89,9 +89,12 @@ def dtype_code(dt: torch.dtype) -> int:
         return DTYPE_BF16
     if dt == torch.float32:
         return DTYPE_F32
+    if dt == torch.float16:
+        return DTYPE_F16
     if dt == torch.float8_e4m3fn:
         return DTYPE_FP8_E4M3
-    raise NotImplementedError(f"dtype {dt} is not supported (bfloat16, float32; float8_e4m3fn for the KV cache)")
+    raise NotImplementedError(f"dtype {dt} is not supported (float32, bfloat16, float16; float8_e4m3fn for the "
+                              "KV cache)")
 
 
 def stream_ptr(device: torch.device) -> int:

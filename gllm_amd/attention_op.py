@@ -1,6 +1,6 @@
 """Drop-in for ``gllm/ops/attention/reference_attention.py`` and
 ``gllm/ops/attention/flash_attention.py``: the dense-bias attention op on the
-HIP kernels (bf16 MFMA or fp32)."""
+HIP kernels (bf16 / fp16 MFMA, or the generic fp32-arithmetic kernel)."""
 from __future__ import annotations
 
 import math

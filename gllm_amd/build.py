@@ -20,11 +20,12 @@ LIB = os.path.join(LIBDIR, "libgllm_attn.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["api.hip", "rope_kv_write.hip", "paged_attention.hip", "attention_f32.hip", "metadata.hip",
-           "qkv_proj.hip"]
+SOURCES = ["paged_attention.hip", "paged_attention_f16.hip", "api.hip", "rope_kv_write.hip", "attention_f32.hip",
+           "metadata.hip", "qkv_proj.hip"]
 NO_CONTRACT = {"rope_kv_write.hip", "attention_f32.hip", "qkv_proj.hip"}
 # MFMA accumulators stay in VGPRs (no per-tile AGPR<->VGPR copies)
-EXTRA = {"paged_attention.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"]}
+EXTRA = {"paged_attention.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"],
+         "paged_attention_f16.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"]}
 COMMON = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     # packed fp32 VALU ops are disabled on purpose for every HIP unit
@@ -58,7 +59,7 @@ def _link(objs, out, extra):
 
 def build(verbose: bool = False) -> str:
     os.makedirs(LIBDIR, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(4, os.cpu_count() or 1)) as ex:
+    with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as ex:
         objs = list(ex.map(_compile, SOURCES))
     # roctx ranges around the entry points
     _link(objs, LIB, ["-L/opt/rocm/lib", "-lrocprofiler-sdk-roctx", "-Wl,-rpath,/opt/rocm/lib"])

@@ -71,6 +71,13 @@ void block_div(int32_t bs, uint32_t* magic, int32_t* shift) {
 }
 constexpr int32_t kMaxBlockSize = 65536;
 
+// Model dtypes (the reference's model_dtype, model.py:64): f32, bf16, f16;
+// cache dtypes (kv_dtype, model.py:75): those and fp8 e4m3fn, any pairing.
+bool model_dtype_ok(int32_t d) { return d == GLLM_DTYPE_F32 || d == GLLM_DTYPE_BF16 || d == GLLM_DTYPE_F16; }
+bool kv_dtype_ok(int32_t d) { return model_dtype_ok(d) || d == GLLM_DTYPE_FP8_E4M3; }
+// 16-bit model dtypes run the MFMA kernels (head dim 64 / 128)
+bool mfma_dtype(int32_t d) { return d == GLLM_DTYPE_BF16 || d == GLLM_DTYPE_F16; }
+
 // CUs of the current device (256 when there is none, e.g. a CPU-only host),
 // queried once per device: plans and projection calls ask on every engine step.
 int device_cus() {
@@ -444,10 +451,8 @@ int gllm_rope_kv_write(const void* q, void* q_out, const void* k, const void* v,
   if (!kv && !q_out) return fail(GLLM_ATTN_EINVAL, "nothing to do: neither k/v nor q_out given");
   if (q_out && !q) return fail(GLLM_ATTN_EINVAL, "q_out given without q");
   if (num_kv_heads <= 0 || num_q_heads <= 0) return fail(GLLM_ATTN_EINVAL, "head counts must be > 0");
-  if (!((dtype == GLLM_DTYPE_BF16 && (kv_dtype == GLLM_DTYPE_BF16 || kv_dtype == GLLM_DTYPE_FP8_E4M3)) ||
-        (dtype == GLLM_DTYPE_F32 &&
-         (kv_dtype == GLLM_DTYPE_F32 || kv_dtype == GLLM_DTYPE_BF16 || kv_dtype == GLLM_DTYPE_FP8_E4M3))))
-    return fail(GLLM_ATTN_EUNSUPPORTED, "dtype/kv_dtype combination %d/%d not supported", dtype, kv_dtype);
+  if (!model_dtype_ok(dtype)) return fail(GLLM_ATTN_EUNSUPPORTED, "model dtype %d (f32, bf16 or f16)", dtype);
+  if (kv && !kv_dtype_ok(kv_dtype)) return fail(GLLM_ATTN_EUNSUPPORTED, "kv_dtype %d (f32, bf16, f16 or fp8 e4m3fn)", kv_dtype);
   const int vec = dtype == GLLM_DTYPE_F32 ? 4 : 8;
   if (head_dim <= 0 || head_dim % (2 * vec) != 0)
     return fail(GLLM_ATTN_EUNSUPPORTED, "head_dim %d must be a positive multiple of %d", head_dim, 2 * vec);
@@ -606,10 +611,10 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
                 num_q_heads, num_kv_heads);
   if (block_size <= 0 || block_size > kMaxBlockSize)
     return fail(GLLM_ATTN_EINVAL, "block_size %d must be in [1, %d]", block_size, kMaxBlockSize);
-  if (dtype != GLLM_DTYPE_BF16 && dtype != GLLM_DTYPE_F32) return fail(GLLM_ATTN_EUNSUPPORTED, "dtype %d", dtype);
+  if (!model_dtype_ok(dtype)) return fail(GLLM_ATTN_EUNSUPPORTED, "model dtype %d (f32, bf16 or f16)", dtype);
   if (head_dim <= 0 || head_dim > 256 || head_dim % 2)
     return fail(GLLM_ATTN_EUNSUPPORTED, "head_dim %d (even, at most 256)", head_dim);
-  const bool mfma = dtype == GLLM_DTYPE_BF16 && (head_dim == 64 || head_dim == 128);
+  const bool mfma = mfma_dtype(dtype) && (head_dim == 64 || head_dim == 128);
   if (split_tokens != GLLM_SPLIT_BALANCED && (split_tokens < 0 || split_tokens % 32))
     return fail(GLLM_ATTN_EINVAL, "split_tokens must be a multiple of 32 or GLLM_SPLIT_BALANCED");
   if (decode_heads_per_wg != 0 && decode_heads_per_wg != 1 && decode_heads_per_wg != 2 &&
@@ -939,11 +944,7 @@ int gllm_paged_attention(const gllm_attn_plan* p, const void* q, int64_t q_row_s
     return fail(GLLM_ATTN_EINVAL, "rope_mode %d", rope_mode);
   if (rope_mode != GLLM_ROPE_NONE && (!rope_cos || !rope_sin || rope_row_stride < p->D / 2))
     return fail(GLLM_ATTN_EINVAL, "rope tables missing or row stride < head_dim / 2");
-  if (dtype == GLLM_DTYPE_BF16 && kv_dtype != GLLM_DTYPE_BF16 && kv_dtype != GLLM_DTYPE_FP8_E4M3)
-    return fail(GLLM_ATTN_EUNSUPPORTED, "bf16 model dtype needs a bf16 or fp8 e4m3 KV cache");
-  if (dtype == GLLM_DTYPE_F32 && kv_dtype != GLLM_DTYPE_F32 && kv_dtype != GLLM_DTYPE_BF16 &&
-      kv_dtype != GLLM_DTYPE_FP8_E4M3)
-    return fail(GLLM_ATTN_EUNSUPPORTED, "kv_dtype %d", kv_dtype);
+  if (!kv_dtype_ok(kv_dtype)) return fail(GLLM_ATTN_EUNSUPPORTED, "kv_dtype %d (f32, bf16, f16 or fp8 e4m3fn)", kv_dtype);
   AttnArgs a{};
   if (int rc = fill_common(a, p->Hq, p->Hkv, p->D, scale, dtype, kv_dtype)) return rc;
   a.q = q; a.q_row_stride = q_row_stride; a.out = out; a.out_row_stride = out_row_stride;
@@ -972,8 +973,11 @@ int gllm_paged_attention(const gllm_attn_plan* p, const void* q, int64_t q_row_s
   a.decode_waves = p->decode_waves;
   a.prefill_waves = p->prefill_waves;
   hipStream_t st = (hipStream_t)stream;
-  if (p->mfma)
-    return hip_check(launch_paged_attention_bf16(a, p->n_prefill_seqs > 0, p->n_decode_seqs > 0, st),
+  // the MFMA kernels read a cache in the model dtype or fp8; a 16-bit model
+  // over an f32 (or the other 16-bit) cache takes the generic kernel, which
+  // rounds each cached value to the model dtype as the reference's gather does
+  if (p->mfma && (kv_dtype == dtype || kv_dtype == GLLM_DTYPE_FP8_E4M3))
+    return hip_check(launch_paged_attention_mfma(a, p->n_prefill_seqs > 0, p->n_decode_seqs > 0, st),
                      "paged attention launch");
   return hip_check(launch_attention_f32(a, false, p->num_seqs, p->max_q, st), "generic attention launch");
 }
@@ -994,7 +998,7 @@ int gllm_attention_dense(const void* q, int64_t q_row_stride, const void* k, int
   if (k_row_stride < (int64_t)num_kv_heads * head_dim || v_row_stride < (int64_t)num_kv_heads * head_dim)
     return fail(GLLM_ATTN_EINVAL, "k/v row stride too small");
   if (bias_row_stride < kv_len) return fail(GLLM_ATTN_EINVAL, "bias row stride < kv_len");
-  if (dtype != GLLM_DTYPE_BF16 && dtype != GLLM_DTYPE_F32) return fail(GLLM_ATTN_EUNSUPPORTED, "dtype %d", dtype);
+  if (!model_dtype_ok(dtype)) return fail(GLLM_ATTN_EUNSUPPORTED, "model dtype %d (f32, bf16 or f16)", dtype);
   if (head_dim <= 0 || head_dim > 256 || head_dim % 2)
     return fail(GLLM_ATTN_EUNSUPPORTED, "head_dim %d (even, at most 256)", head_dim);
   if (kv_len == 0 && batch * q_len > 0) return fail(GLLM_ATTN_EINVAL, "kv_len == 0 (softmax over no keys)");
@@ -1006,8 +1010,8 @@ int gllm_attention_dense(const void* q, int64_t q_row_stride, const void* k, int
   a.bias = bias; a.bias_batch_stride = bias_batch_stride; a.bias_row_stride = bias_row_stride;
   a.dense_T = kv_len; a.dense_Tq = q_len;
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == GLLM_DTYPE_BF16 && (head_dim == 64 || head_dim == 128))
-    return hip_check(launch_dense_attention_bf16(a, batch, q_len, st), "dense attention launch");
+  if (mfma_dtype(dtype) && (head_dim == 64 || head_dim == 128))
+    return hip_check(launch_dense_attention_mfma(a, batch, q_len, st), "dense attention launch");
   return hip_check(launch_attention_f32(a, true, batch, q_len, st), "generic dense attention launch");
 }
 

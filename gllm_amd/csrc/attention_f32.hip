@@ -1,10 +1,13 @@
 // Generic attention: paged decode/prefill and the dense-bias op for fp32
-// models (benchmark config (a)) and for bf16 models whose head dim the MFMA
-// kernels do not take (not 64 or 128; up to 256).  One wave per (query head,
-// query row, sequence), 64 keys per step, exact online softmax (expf) in
-// fp32.  Compiled with -ffp-contract=off so the q rotation rounds each op
-// like the reference (gllm/model/layers/attention.py:105-118): in fp32, or to
-// bf16 after every op for a bf16 model.
+// models (benchmark config (a)), for bf16 / fp16 models whose head dim the
+// MFMA kernels do not take (not 64 or 128; up to 256), and for a 16-bit model
+// over a cache of another dtype (f32, or the other 16-bit type).  One wave
+// per (query head, query row, sequence), 64 keys per step, exact online
+// softmax (expf) in fp32.  Compiled with -ffp-contract=off so the q rotation
+// rounds each op like the reference (gllm/model/layers/attention.py:105-118):
+// in fp32, or to the 16-bit model dtype after every op.
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 
@@ -13,6 +16,7 @@ namespace gllm {
 template <typename KV> __device__ __forceinline__ float ldkv(const KV* p);
 template <> __device__ __forceinline__ float ldkv<float>(const float* p) { return *p; }
 template <> __device__ __forceinline__ float ldkv<__bf16>(const __bf16* p) { return (float)*p; }
+template <> __device__ __forceinline__ float ldkv<_Float16>(const _Float16* p) { return (float)*p; }
 // fp8 e4m3fn cache: exact widening (the reference's .to(model dtype) after the gather)
 template <> __device__ __forceinline__ float ldkv<fp8e4m3>(const fp8e4m3* p) { return __builtin_amdgcn_cvt_f32_fp8((int)p->bits, 0); }
 
@@ -20,10 +24,26 @@ template <> __device__ __forceinline__ float ldkv<fp8e4m3>(const fp8e4m3* p) { r
 template <typename QT> __device__ __forceinline__ float rnd(float x);
 template <> __device__ __forceinline__ float rnd<float>(float x) { return x; }
 template <> __device__ __forceinline__ float rnd<__bf16>(float x) { return round_bf16(x); }
+template <> __device__ __forceinline__ float rnd<_Float16>(float x) { return (float)(_Float16)x; }
 template <typename QT> __device__ __forceinline__ void stq(QT* p, float x);
 template <> __device__ __forceinline__ void stq<float>(float* p, float x) { *p = x; }
 template <> __device__ __forceinline__ void stq<__bf16>(__bf16* p, float x) {
   *reinterpret_cast<uint16_t*>(p) = (uint16_t)pack_bf16x2(x, 0.f);
+}
+template <> __device__ __forceinline__ void stq<_Float16>(_Float16* p, float x) { *p = (_Float16)x; }
+
+// A cached value as the reference's gather reads it: cast to the model dtype
+// (attention.py:169-170, .to(q.dtype)).  Exact when the cache holds the model
+// dtype, fp8 e4m3fn (a subset of every model dtype) or feeds an fp32 model;
+// rounded to nearest even for an f32 cache (or the other 16-bit type) under
+// a 16-bit model.
+template <typename KV, typename QT>
+__device__ __forceinline__ float kvld(const KV* p) {
+  constexpr bool exact = std::is_same<QT, float>::value || std::is_same<KV, QT>::value ||
+                         std::is_same<KV, fp8e4m3>::value;
+  const float x = ldkv<KV>(p);
+  if constexpr (exact) return x;
+  else return rnd<QT>(x);
 }
 
 // One 4-wave workgroup per (query head, query row, sequence).  Keys go 64 at
@@ -128,7 +148,7 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < NI; ++i) {   // every lane loads (dims past D re-read dim D - 1): no branch per load
           const int d = lane + 64 * i;
-          const float v = ldkv<KV>(vp + min(d, D - 1));
+          const float v = kvld<KV, QT>(vp + min(d, D - 1));
           vv[u][i] = d < D ? v : 0.f;
         }
       }
@@ -148,7 +168,7 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
         for (int c = 0; c < 16; ++c) {
           const int cs = min(4 * c, D - 4);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) kv[c][j] = ldkv<KV>(kp + cs + j);
+          for (int j = 0; j < 4; ++j) kv[c][j] = kvld<KV, QT>(kp + cs + j);
         }
 #pragma unroll
         for (int c = 0; c < 16; ++c) {
@@ -160,10 +180,10 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
 #pragma unroll 16
         for (; d + 4 <= D; d += 4) {
           const f32x4 qv = *reinterpret_cast<const f32x4*>(qs + d);
-          dot += qv[0] * ldkv<KV>(kp + d) + qv[1] * ldkv<KV>(kp + d + 1) + qv[2] * ldkv<KV>(kp + d + 2) +
-                 qv[3] * ldkv<KV>(kp + d + 3);
+          dot += qv[0] * kvld<KV, QT>(kp + d) + qv[1] * kvld<KV, QT>(kp + d + 1) + qv[2] * kvld<KV, QT>(kp + d + 2) +
+                 qv[3] * kvld<KV, QT>(kp + d + 3);
         }
-        for (; d < D; ++d) dot += qs[d] * ldkv<KV>(kp + d);   // head dims not a multiple of 4
+        for (; d < D; ++d) dot += qs[d] * kvld<KV, QT>(kp + d);   // head dims not a multiple of 4
       }
       s = dot * a.scale;
       if (DENSE) s += (float)brow[p];
@@ -238,24 +258,31 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
   }
 }
 
-template <int NI>
-static void launch_f32_ni(const AttnArgs& a, bool dense, dim3 grid, hipStream_t st) {
+// Cache dtype KV under model dtype QT (paged), or QT throughout (dense).
+template <typename QT, int NI>
+static hipError_t launch_f32_qt(const AttnArgs& a, bool dense, dim3 grid, hipStream_t st) {
   const dim3 block(256);
-  if (a.dtype == kBF16) {                 // bf16 model (head dims the MFMA kernels do not take)
-    if (dense)
-      hipLaunchKernelGGL((attn_f32_kernel<true, __bf16, __bf16, NI>), grid, block, 0, st, a);
-    else if (a.kv_dtype == kFP8)
-      hipLaunchKernelGGL((attn_f32_kernel<false, fp8e4m3, __bf16, NI>), grid, block, 0, st, a);
-    else
-      hipLaunchKernelGGL((attn_f32_kernel<false, __bf16, __bf16, NI>), grid, block, 0, st, a);
-  } else if (dense) {
-    hipLaunchKernelGGL((attn_f32_kernel<true, float, float, NI>), grid, block, 0, st, a);
-  } else if (a.kv_dtype == kF32) {
-    hipLaunchKernelGGL((attn_f32_kernel<false, float, float, NI>), grid, block, 0, st, a);
-  } else if (a.kv_dtype == kFP8) {
-    hipLaunchKernelGGL((attn_f32_kernel<false, fp8e4m3, float, NI>), grid, block, 0, st, a);
-  } else {
-    hipLaunchKernelGGL((attn_f32_kernel<false, __bf16, float, NI>), grid, block, 0, st, a);
+  if (dense) {
+    hipLaunchKernelGGL((attn_f32_kernel<true, QT, QT, NI>), grid, block, 0, st, a);
+    return hipGetLastError();
+  }
+  switch (a.kv_dtype) {
+    case kF32: hipLaunchKernelGGL((attn_f32_kernel<false, float, QT, NI>), grid, block, 0, st, a); break;
+    case kBF16: hipLaunchKernelGGL((attn_f32_kernel<false, __bf16, QT, NI>), grid, block, 0, st, a); break;
+    case kF16: hipLaunchKernelGGL((attn_f32_kernel<false, _Float16, QT, NI>), grid, block, 0, st, a); break;
+    case kFP8: hipLaunchKernelGGL((attn_f32_kernel<false, fp8e4m3, QT, NI>), grid, block, 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int NI>
+static hipError_t launch_f32_ni(const AttnArgs& a, bool dense, dim3 grid, hipStream_t st) {
+  switch (a.dtype) {
+    case kF32: return launch_f32_qt<float, NI>(a, dense, grid, st);
+    case kBF16: return launch_f32_qt<__bf16, NI>(a, dense, grid, st);
+    case kF16: return launch_f32_qt<_Float16, NI>(a, dense, grid, st);
+    default: return hipErrorInvalidValue;
   }
 }
 
@@ -263,11 +290,8 @@ hipError_t launch_attention_f32(const AttnArgs& a, bool dense, int B, int max_q,
   if (B == 0 || max_q == 0) return hipSuccess;
   if (a.head_dim <= 0 || a.head_dim > 256) return hipErrorInvalidValue;
   const dim3 grid(a.num_q_heads, max_q, B);
-  if (a.head_dim <= 64 && a.head_dim % 4 == 0)
-    launch_f32_ni<1>(a, dense, grid, st);
-  else
-    launch_f32_ni<4>(a, dense, grid, st);
-  return hipGetLastError();
+  if (a.head_dim <= 64 && a.head_dim % 4 == 0) return launch_f32_ni<1>(a, dense, grid, st);
+  return launch_f32_ni<4>(a, dense, grid, st);
 }
 
 }  // namespace gllm

@@ -130,6 +130,111 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
                fp8x2_to_bf16x2<true>(w1)};
 }
 
+// ---------------------------------------------------------------- 16-bit model types
+// The MFMA kernels take a bf16 or an fp16 model (T = __bf16 or _Float16).
+// Operands move as raw 32-bit words (two elements each); E16<T> converts,
+// rounds (RNE, like torch's stores in T) and multiplies per type.
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+
+template <typename T> struct E16;
+template <> struct E16<__bf16> {
+  static constexpr bool kF16 = false;
+  __device__ static uint32_t pack2(float lo, float hi) { return pack_bf16x2(lo, hi); }
+  __device__ static float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  __device__ static float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  __device__ static f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  }
+  __device__ static f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  }
+  __device__ static f32x4 mfma16k16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c,
+                                                     0, 0, 0);
+  }
+  // 2 fp8 e4m3 values (bytes 2 HI, 2 HI + 1 of w) -> 2 elements (exact)
+  template <bool HI> __device__ static uint32_t fp8x2(uint32_t w) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, HI));
+  }
+  // c + lo + hi (one v_dot2c against 1.0)
+  __device__ static float add2(uint32_t w, float c) {
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, c, false);
+  }
+};
+template <> struct E16<_Float16> {
+  static constexpr bool kF16 = true;
+  __device__ static uint32_t pack2(float lo, float hi) {   // v_cvt_pk_f16_f32: RNE, overflow to inf
+    f16x2 r;
+    r[0] = (_Float16)lo;
+    r[1] = (_Float16)hi;
+    return __builtin_bit_cast(uint32_t, r);
+  }
+  __device__ static float lo(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w)[0]; }
+  __device__ static float hi(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w)[1]; }
+  __device__ static f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
+  }
+  __device__ static f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
+  }
+  __device__ static f32x4 mfma16k16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c,
+                                                 0, 0, 0);
+  }
+  // every e4m3 value is an fp16 value: exact
+  template <bool HI> __device__ static uint32_t fp8x2(uint32_t w) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, HI));
+  }
+  __device__ static float add2(uint32_t w, float c) {
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, c, false);
+  }
+};
+
+template <typename T>
+__device__ __forceinline__ void unpack8(const u32x4 w, float* v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = E16<T>::lo(w[i]);
+    v[2 * i + 1] = E16<T>::hi(w[i]);
+  }
+}
+template <typename T>
+__device__ __forceinline__ u32x4 pack8(const float* v) {
+  return u32x4{E16<T>::pack2(v[0], v[1]), E16<T>::pack2(v[2], v[3]), E16<T>::pack2(v[4], v[5]),
+               E16<T>::pack2(v[6], v[7])};
+}
+// two values rounded to T with one convert
+template <typename T>
+__device__ __forceinline__ void round2(float& a, float& b) {
+  const uint32_t w = E16<T>::pack2(a, b);
+  a = E16<T>::lo(w);
+  b = E16<T>::hi(w);
+}
+// one rotate-half pair with every op rounded to T (attention.py:105-118)
+template <typename T>
+__device__ __forceinline__ void rope_pair(float& x1, float& x2, float c, float s) {
+  float a = __fmul_rn(x1, c), b = __fmul_rn(x2, s), e = __fmul_rn(x1, s), f = __fmul_rn(x2, c);
+  round2<T>(a, b);
+  round2<T>(e, f);
+  x1 = __fsub_rn(a, b);
+  x2 = __fadd_rn(e, f);
+  round2<T>(x1, x2);
+}
+// 8 fp8 bytes -> 8 elements of T (exact)
+template <typename T>
+__device__ __forceinline__ u32x4 fp8x8_to(uint32_t w0, uint32_t w1) {
+  return u32x4{E16<T>::template fp8x2<false>(w0), E16<T>::template fp8x2<true>(w0),
+               E16<T>::template fp8x2<false>(w1), E16<T>::template fp8x2<true>(w1)};
+}
+
 // ---------------------------------------------------------------- memory
 // Direct global -> LDS copy of 16 bytes per lane: lane l's bytes land at
 // lds_base + 16 l (lds_base wave-uniform, in M0).  Written as inline asm so
@@ -187,14 +292,6 @@ __device__ __forceinline__ float sum_xor32(float x) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// c + lo + hi of two packed bf16 values (one v_dot2c_f32_bf16 against 1.0):
-// softmax row sums taken over the bf16-rounded p that the P V MFMA
-// multiplies, so numerator and denominator weigh every key alike.
-__device__ __forceinline__ float add_bf16x2(uint32_t w, float c) {
-  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, c, false);
-}
 
 // Division by the KV block size (any size >= 1): floor(p / bs) for
 // 0 <= p < 2^31 is umulhi(2p, magic) >> shift with k = ceil(log2 bs),

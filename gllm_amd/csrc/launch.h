@@ -7,7 +7,7 @@
 
 namespace gllm {
 
-enum : int32_t { kF32 = 0, kBF16 = 1, kFP8 = 2 };   // kFP8: OCP e4m3fn (KV cache only)
+enum : int32_t { kF32 = 0, kBF16 = 1, kFP8 = 2, kF16 = 3 };   // kFP8: OCP e4m3fn (KV cache only)
 
 struct RopeKVWriteArgs {
   const void* q;            // [N, q_row_stride] model dtype, heads at h*D
@@ -138,8 +138,10 @@ size_t qkv_workspace_bytes(int64_t num_tokens, int hidden, int heads, int head_d
 hipError_t launch_rope_kv_write(const RopeKVWriteArgs& a, hipStream_t stream);
 hipError_t launch_qkv_rope_write(const QKVArgs& a, hipStream_t stream);
 hipError_t launch_build_metadata(const MetadataArgs& a, hipStream_t stream);
-hipError_t launch_paged_attention_bf16(const AttnArgs& a, bool has_prefill, bool has_decode, hipStream_t stream);
-hipError_t launch_dense_attention_bf16(const AttnArgs& a, int B, int Tq, hipStream_t stream);
+// MFMA kernels: bf16 or fp16 model (a.dtype), head dim 64 or 128, cache in
+// the model dtype or fp8 e4m3fn
+hipError_t launch_paged_attention_mfma(const AttnArgs& a, bool has_prefill, bool has_decode, hipStream_t stream);
+hipError_t launch_dense_attention_mfma(const AttnArgs& a, int B, int Tq, hipStream_t stream);
 hipError_t launch_attention_f32(const AttnArgs& a, bool dense, int B, int max_q, hipStream_t stream);
 hipError_t launch_fill_zero_i32(int32_t* p, int64_t n, hipStream_t stream);
 

@@ -25,14 +25,13 @@
 
 namespace gllm {
 
-// Rotate-half RoPE on 8 pairs, each op rounded to bf16 like the reference's
-// torch ops (gllm/model/layers/attention.py:105-118).
-__device__ __forceinline__ void rope8_bf16(float* x1, float* x2, const float* c, const float* s) {
+// Rotate-half RoPE on 8 pairs, each op rounded to the model dtype T like the
+// reference's torch ops (gllm/model/layers/attention.py:105-118).
+template <typename T>
+__device__ __forceinline__ void rope8(float* x1, float* x2, const float* c, const float* s) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) rope_pair_bf16(x1[i], x2[i], c[i], s[i]);
+  for (int i = 0; i < 8; ++i) rope_pair<T>(x1[i], x2[i], c[i], s[i]);
 }
-
-__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 w) { return __builtin_bit_cast(bf16x8, w); }
 
 
 // ============================================================== decode
@@ -48,10 +47,6 @@ template <int D, int NW> struct DecodeCfg {
   static constexpr int kLdsBytes = kStage > kMerge ? kStage : kMerge;
 };
 
-__device__ __forceinline__ f32x4 mfma16k16(u32x2 a, u32x2 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b),
-                                                   c, 0, 0, 0);
-}
 
 // One (HW x KW)-wave workgroup per (sequence, context split, group of HW kv
 // heads).  Wave w serves kv head HW * group + w % HW and takes the split's
@@ -76,11 +71,11 @@ template <bool KV8>
 __device__ __forceinline__ int chunk_dim(int kk, int grp) {
   return KV8 ? 64 * (kk >> 1) + 16 * grp + 8 * (kk & 1) : 32 * kk + 8 * grp;
 }
-template <bool KV8>
-__device__ __forceinline__ u32x4 chunk_bf16(const u32x4* raw, int kk) {
+template <typename T, bool KV8>
+__device__ __forceinline__ u32x4 chunk_elems(const u32x4* raw, int kk) {
   if constexpr (KV8) {
     const u32x4 w = raw[kk >> 1];
-    return (kk & 1) ? fp8x8_to_bf16x8(w[2], w[3]) : fp8x8_to_bf16x8(w[0], w[1]);
+    return (kk & 1) ? fp8x8_to<T>(w[2], w[3]) : fp8x8_to<T>(w[0], w[1]);
   } else {
     return raw[kk];
   }
@@ -97,7 +92,7 @@ struct DecodeTask {
 
 // Runs one task with every wave of the workgroup; returns with the workgroup
 // converged (no early exit), so a workgroup can run several tasks in a row.
-template <int D, int HW, int KW, bool KV8>
+template <typename T, int D, int HW, int KW, bool KV8>
 __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask& tk, char* lds, int* ticket_lds) {
   constexpr int NW = HW * KW;
   constexpr int E = KV8 ? 1 : 2;   // bytes per cached element
@@ -144,15 +139,15 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
   const int nblk = (int)div_bs((uint32_t)(kend - 1), a.block_magic, a.block_shift) - blk0 + 1;
   const int32_t* bt = a.block_table + (int64_t)seq * a.block_table_stride + blk0;
   const uint32_t bid = tid < nblk ? (uint32_t)bt[tid] : 0u;
-  const __bf16* qp = (const __bf16*)a.q + qrow * a.q_row_stride + (int64_t)qh * D;
+  const T* qp = (const T*)a.q + qrow * a.q_row_stride + (int64_t)qh * D;
   u32x4 qraw[NK], praw[kPairInLane ? 1 : NK], craw[NC], sraw[NC];
 #pragma unroll
   for (int kk = 0; kk < NK; ++kk) qraw[kk] = ld16(qp + chunk_dim<KV8>(kk, grp));
   const bool rope = a.rope_mode != kRopeNone;
   if (rope) {
     const int64_t crow = a.rope_mode == kRopeByPosition ? (int64_t)vis : qrow;
-    const __bf16* cp = (const __bf16*)a.rope_cos + crow * a.rope_row_stride;
-    const __bf16* sp = (const __bf16*)a.rope_sin + crow * a.rope_row_stride;
+    const T* cp = (const T*)a.rope_cos + crow * a.rope_row_stride;
+    const T* sp = (const T*)a.rope_sin + crow * a.rope_row_stride;
 #pragma unroll
     for (int kk = 0; kk < NC; ++kk) {
       const int d = chunk_dim<KV8>(kk, grp) & (D / 2 - 1);
@@ -167,38 +162,38 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
   if (tid < nblk) lbid[tid] = bid < (uint64_t)a.num_blocks ? (int32_t)bid : 0;  // never address outside the pool
 
   // Q as the B operand of S^T = K Q^T: lane holds Q[row n][chunk_dim(kk) + i].
-  bf16x8 qB[NK];
+  u32x4 qB[NK];
   {
     float x[NK][8];
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) unpack_bf16x8(qraw[kk], x[kk]);
+    for (int kk = 0; kk < NK; ++kk) unpack8<T>(qraw[kk], x[kk]);
     if (rope) {
       if constexpr (kPairInLane) {
 #pragma unroll
         for (int kk = 0; kk < NK / 2; ++kk) {
           float c[8], s[8];
-          unpack_bf16x8(craw[kk], c);
-          unpack_bf16x8(sraw[kk], s);
-          rope8_bf16(x[kk], x[kk + NK / 2], c, s);
+          unpack8<T>(craw[kk], c);
+          unpack8<T>(sraw[kk], s);
+          rope8<T>(x[kk], x[kk + NK / 2], c, s);
         }
       } else {
-        // the same roundings as rope8_bf16, one half of the pair per lane
+        // the same roundings as rope8, one half of the pair per lane
         const bool first = chunk_dim<KV8>(0, grp) < D / 2;
 #pragma unroll
         for (int kk = 0; kk < NK; ++kk) {
           float c[8], s[8], xp[8];
-          unpack_bf16x8(craw[kk], c);
-          unpack_bf16x8(sraw[kk], s);
-          unpack_bf16x8(praw[kk], xp);
+          unpack8<T>(craw[kk], c);
+          unpack8<T>(sraw[kk], s);
+          unpack8<T>(praw[kk], xp);
 #pragma unroll
           for (int i = 0; i < 8; i += 2) {
             float u0 = __fmul_rn(x[kk][i], c[i]), v0 = __fmul_rn(xp[i], s[i]);
             float u1 = __fmul_rn(x[kk][i + 1], c[i + 1]), v1 = __fmul_rn(xp[i + 1], s[i + 1]);
-            round2_bf16(u0, v0);
-            round2_bf16(u1, v1);
+            round2<T>(u0, v0);
+            round2<T>(u1, v1);
             float r0 = first ? __fsub_rn(u0, v0) : __fadd_rn(u0, v0);
             float r1 = first ? __fsub_rn(u1, v1) : __fadd_rn(u1, v1);
-            round2_bf16(r0, r1);
+            round2<T>(r0, r1);
             x[kk][i] = r0;
             x[kk][i + 1] = r1;
           }
@@ -209,7 +204,7 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
     for (int kk = 0; kk < NK; ++kk) {
       if (!row_ok)
         for (int i = 0; i < 8; ++i) x[kk][i] = 0.f;
-      qB[kk] = to_bf16x8(x[kk]);
+      qB[kk] = pack8<T>(x[kk]);
     }
   }
   __syncthreads();
@@ -247,10 +242,10 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
     const int kb = t < ntw ? kbeg + 16 * (ki + KW * t) : kend;
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) s = mfma16(as_bf16x8(chunk_bf16<KV8>(kd, kk)), qB[kk], s);
+    for (int kk = 0; kk < NK; ++kk) s = E16<T>::mfma16(chunk_elems<T, KV8>(kd, kk), qB[kk], s);
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk)
-      *reinterpret_cast<u32x4*>(ldsV + n * RB + chunk_dim<KV8>(kk, grp) * 2) = chunk_bf16<KV8>(vd, kk);
+      *reinterpret_cast<u32x4*>(ldsV + n * RB + chunk_dim<KV8>(kk, grp) * 2) = chunk_elems<T, KV8>(vd, kk);
     // lane holds S[key kb + 4grp + j][row n]
     float p[4];
 #pragma unroll
@@ -278,11 +273,11 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
     const float mu = m == kNegInf ? 0.f : m;
 #pragma unroll
     for (int j = 0; j < 4; ++j) p[j] = fast_exp2(p[j] - mu);
-    const u32x2 pb = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
-    lsum = add_bf16x2(pb[1], add_bf16x2(pb[0], lsum));   // the rounded p the MFMA sees
+    const u32x2 pb = {E16<T>::pack2(p[0], p[1]), E16<T>::pack2(p[2], p[3])};
+    lsum = E16<T>::add2(pb[1], E16<T>::add2(pb[0], lsum));   // the rounded p the MFMA sees
     const char* vrow = ldsV + (4 * grp + (n >> 2)) * RB + 4 * (n & 3) * 2;
 #pragma unroll
-    for (int d = 0; d < ND; ++d) acc[d] = mfma16k16(lds_read_tr16(vrow + 32 * d), pb, acc[d]);
+    for (int d = 0; d < ND; ++d) acc[d] = E16<T>::mfma16k16(lds_read_tr16(vrow + 32 * d), pb, acc[d]);
   };
 
   // The ring issues loads unconditionally (tiles past the end read one
@@ -353,11 +348,11 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
   const bool wr = lead && row_ok;
   if (tk.nseg == 1) {
     if (wr) {
-      __bf16* op = (__bf16*)a.out + qrow * a.out_row_stride + (int64_t)qh * D + 4 * grp;
+      T* op = (T*)a.out + qrow * a.out_row_stride + (int64_t)qh * D + 4 * grp;
       const float inv = 1.f / lt;
 #pragma unroll
       for (int d = 0; d < ND; ++d)
-        st8(op + 16 * d, u32x2{pack_bf16x2(acc[d][0] * inv, acc[d][1] * inv), pack_bf16x2(acc[d][2] * inv, acc[d][3] * inv)});
+        st8(op + 16 * d, u32x2{E16<T>::pack2(acc[d][0] * inv, acc[d][1] * inv), E16<T>::pack2(acc[d][2] * inv, acc[d][3] * inv)});
     }
     return;
   }
@@ -445,16 +440,16 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
   }
   if (!row_ok) return;   // ps == 0 lanes: mr == n
   const float inv = 1.f / Lx;
-  __bf16* op = (__bf16*)a.out + qrow * a.out_row_stride + (int64_t)qh * D + 4 * grp;
+  T* op = (T*)a.out + qrow * a.out_row_stride + (int64_t)qh * D + 4 * grp;
 #pragma unroll
   for (int d = 0; d < ND; ++d)
-    st8(op + 16 * d, u32x2{pack_bf16x2(ox[d][0] * inv, ox[d][1] * inv), pack_bf16x2(ox[d][2] * inv, ox[d][3] * inv)});
+    st8(op + 16 * d, u32x2{E16<T>::pack2(ox[d][0] * inv, ox[d][1] * inv), E16<T>::pack2(ox[d][2] * inv, ox[d][3] * inv)});
 }
 
 // One decode work item of the split-launch planner (split it.a of the
 // sequence's it.nsplits equal key ranges; split partials merged by
 // merge_splits_kernel).
-template <int D, int HW, int KW, bool KV8>
+template <typename T, int D, int HW, int KW, bool KV8>
 __device__ __forceinline__ void decode_wg(const AttnArgs& a, const WorkItem& it, char* lds) {
   DecodeTask tk;
   tk.seq = it.seq;
@@ -470,12 +465,12 @@ __device__ __forceinline__ void decode_wg(const AttnArgs& a, const WorkItem& it,
   tk.pbase = it.partial_base + tk.hg * HW * it.nsplits;
   tk.ord = it.a;
   tk.ticket = -1;
-  decode_task<D, HW, KW, KV8>(a, tk, lds, nullptr);
+  decode_task<T, D, HW, KW, KV8>(a, tk, lds, nullptr);
 }
 
 // Combines the split partials of every (sequence, kv head) whose sequence
 // was split: one wave per (sequence, kv head); softmax-weighted (LSE) merge.
-template <int D>
+template <typename T, int D>
 __global__ void __launch_bounds__(64) merge_splits_kernel(AttnArgs a) {
   const int seq = blockIdx.x / a.num_kv_heads, kvh = blockIdx.x - seq * a.num_kv_heads;
   const SeqInfo si = a.seqs[seq];
@@ -499,8 +494,8 @@ __global__ void __launch_bounds__(64) merge_splits_kernel(AttnArgs a) {
     }
     const float inv = 1.f / Ls;
     const int rr = row / G, gg = row - rr * G;
-    __bf16* op = (__bf16*)a.out + (si.q_row_start + rr) * a.out_row_stride + (int64_t)(kvh * G + gg) * D + d4;
-    st8(op, u32x2{pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv)});
+    T* op = (T*)a.out + (si.q_row_start + rr) * a.out_row_stride + (int64_t)(kvh * G + gg) * D + d4;
+    st8(op, u32x2{E16<T>::pack2(o[0] * inv, o[1] * inv), E16<T>::pack2(o[2] * inv, o[3] * inv)});
   }
 }
 
@@ -547,7 +542,7 @@ __device__ __forceinline__ int pf_swz(int r) {
 // Paged mode: keys through the block table, causal mask on diagonal tiles
 // only.  Dense mode (DENSE): keys from k/v [B, T, Hkv, D], additive bias
 // [B, T_q, T] on every tile.
-template <int D, bool DENSE, int NW, int NS, bool KV8>
+template <typename T, int D, bool DENSE, int NW, int NS, bool KV8>
 __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it, int seq, int kvh, int wgrp, char* lds) {
   static_assert(!(DENSE && KV8), "the dense op has no cache");
   using Cfg = PrefillCfg<D, NS>;
@@ -561,17 +556,17 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n = lane & 31, h = lane >> 5;
 
-  int ctx, qlen, T;
+  int ctx, qlen, TK;
   int64_t qstart;
   if (DENSE) {
     ctx = 0;
     qlen = a.dense_Tq;
-    T = a.dense_T;
+    TK = a.dense_T;
     qstart = (int64_t)seq * a.dense_Tq;
   } else {
     ctx = it.ctx_len;
     qlen = it.q_len;
-    T = ctx + qlen;
+    TK = ctx + qlen;
     qstart = it.q_row_start;
   }
   const int G = a.num_q_heads / a.num_kv_heads;
@@ -582,8 +577,8 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   const int rblk = wact ? combo / G : 0;
   const int r0 = rblk * 32;
   const int last_combo = min(wgrp * NW + NW - 1, G * nrb - 1);
-  const int kend_wg = DENSE ? T : ctx + min(qlen - 1, (last_combo / G) * 32 + 31) + 1;
-  const int kend_w = DENSE ? T : ctx + min(qlen - 1, r0 + 31) + 1;
+  const int kend_wg = DENSE ? TK : ctx + min(qlen - 1, (last_combo / G) * 32 + 31) + 1;
+  const int kend_w = DENSE ? TK : ctx + min(qlen - 1, r0 + 31) + 1;
   const int r = r0 + n;
   const bool row_ok = wact && r < qlen;
   const int rr = min(r, qlen - 1);
@@ -606,13 +601,13 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   u32x4 qraw[NQ], craw[NQ / 2], sraw[NQ / 2];
   const bool q_rope = !DENSE && a.rope_mode != kRopeNone;
   {
-    const __bf16* qp = (const __bf16*)a.q + qrow * a.q_row_stride + (int64_t)qh * D + 8 * h;
+    const T* qp = (const T*)a.q + qrow * a.q_row_stride + (int64_t)qh * D + 8 * h;
 #pragma unroll
     for (int kk = 0; kk < NQ; ++kk) qraw[kk] = ld16(qp + 16 * kk);
     if (q_rope) {
       const int64_t crow = a.rope_mode == kRopeByPosition ? (int64_t)vis : qrow;
-      const __bf16* cp = (const __bf16*)a.rope_cos + crow * a.rope_row_stride + 8 * h;
-      const __bf16* sp = (const __bf16*)a.rope_sin + crow * a.rope_row_stride + 8 * h;
+      const T* cp = (const T*)a.rope_cos + crow * a.rope_row_stride + 8 * h;
+      const T* sp = (const T*)a.rope_sin + crow * a.rope_row_stride + 8 * h;
 #pragma unroll
       for (int kk = 0; kk < NQ / 2; ++kk) {
         craw[kk] = ld16(cp + 16 * kk);
@@ -620,7 +615,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
       }
     }
   }
-  bf16x8 qB[NQ];                // filled once the first tile copies are issued
+  u32x4 qB[NQ];                 // filled once the first tile copies are issued
 
   // Per-lane byte offsets inside a stage (tile-invariant; the stage and the
   // half / 16-key group go into the instructions' immediate offsets).
@@ -713,7 +708,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   auto fp8_put = [&](int stage, int i, int v) {
     const int sg = i * NW + wave;
     *reinterpret_cast<u32x4*>(lds + v * Cfg::kVBase + stage * Cfg::kTile + sg * 1024 + lane * 16) =
-        fp8x8_to_bf16x8(f8st[i][v][0], f8st[i][v][1]);
+        fp8x8_to<T>(f8st[i][v][0], f8st[i][v][1]);
   };
   auto dma_issue = [&](int ts, int stage, const uint32_t (&blk)[CHD]) {
     if (KV8) fp8_fetch(ts, blk);
@@ -755,16 +750,20 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   // it (some p > 2^T) sends the wave into a rare fix-up that recomputes the
   // half's S from LDS, moves the reference of every row whose max passed T up
   // to that max (O and l rescaled by 2^-max, exactly) and recomputes p.  With
-  // T = 64, p <= 2^64 keeps l and O far from fp32 overflow.  Numerator and
-  // denominator share r, so the result is the exact softmax.
+  // T = 64, p <= 2^64 keeps l and O far from fp32 overflow.  An fp16 model
+  // takes P in fp16 (largest value 65504): T = 15, and r starts at m1
+  // itself, so p <= 2^15 and the keys that carry the row never fall into
+  // fp16's subnormal range.  Numerator and denominator share r, so the result
+  // is the exact softmax.
   //
   // Dense (arbitrary bias) mode: lazy running max (the max only moves when a
   // row's max exceeds it by more than 8, so p <= 2^8); scale, bias and the
   // tile's starting offset -m enter one FMA per score, so the exponent is
   // s - m directly (a subtract of the max's move otherwise, rare).
   constexpr bool kFast = !DENSE;
-  constexpr float kT = 64.f;
-  constexpr float kTwoT = 18446744073709551616.f;   // 2^64
+  constexpr bool kF16 = E16<T>::kF16;
+  constexpr float kT = kF16 ? 15.f : 64.f;
+  constexpr float kTwoT = kF16 ? 32768.f : 18446744073709551616.f;   // 2^T
   float rref = 0.f;              // paged mode: the row's reference r (log2 units)
   struct Soft { float alpha, dlt, psum; };
   auto row_max = [&](const f32x16& s) {
@@ -792,7 +791,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
     if (mask) apply_mask(s, k0);
     if (first) {
       const float m1 = row_max(s);
-      rref = (m1 >= -kT && m1 <= kT) || m1 == kNegInf ? 0.f : m1;
+      rref = (!kF16 && m1 >= -kT && m1 <= kT) || m1 == kNegInf ? 0.f : m1;
       if (__builtin_amdgcn_ballot_w64(rref != 0.f)) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) s[j] -= rref;
@@ -801,11 +800,11 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   };
   auto sm_max = [&](f32x16& s, int k0, bool mask, Soft& q) {
     if (DENSE) {
-      const __bf16* bp = (const __bf16*)a.bias + (int64_t)seq * a.bias_batch_stride + (int64_t)rr * a.bias_row_stride;
+      const T* bp = (const T*)a.bias + (int64_t)seq * a.bias_batch_stride + (int64_t)rr * a.bias_row_stride;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {   // bias in natural-log units: to log2 units like the scaled scores
         const int key = k0 + 8 * (j >> 2) + 4 * h + (j & 3);
-        const float bv = key < T ? (float)bp[key] : kNegInf;
+        const float bv = key < TK ? (float)bp[key] : kNegInf;
         s[j] = __builtin_fmaf(s[j], sl2, __builtin_fmaf(bv, kLog2e, sbase));
       }
     } else if (mask) {
@@ -827,29 +826,29 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
     for (int j = j0; j < j0 + 4; ++j) s[j] = fast_exp2(s[j]);
   };
   // row sum of the half's bf16-rounded p (the values the P V MFMA takes)
-  auto sm_sum = [&](const bf16x8* pb, Soft& q) {
-    const u32x4 w0 = __builtin_bit_cast(u32x4, pb[0]), w1 = __builtin_bit_cast(u32x4, pb[1]);
-    float a0 = add_bf16x2(w0[0], 0.f), a1 = add_bf16x2(w1[0], 0.f);
+  auto sm_sum = [&](const u32x4* pb, Soft& q) {
+    const u32x4 w0 = pb[0], w1 = pb[1];
+    float a0 = E16<T>::add2(w0[0], 0.f), a1 = E16<T>::add2(w1[0], 0.f);
 #pragma unroll
     for (int e = 1; e < 4; ++e) {
-      a0 = add_bf16x2(w0[e], a0);
-      a1 = add_bf16x2(w1[e], a1);
+      a0 = E16<T>::add2(w0[e], a0);
+      a1 = E16<T>::add2(w1[e], a1);
     }
     q.psum = a0 + a1;
     if (!kFast) lsum = __builtin_fmaf(lsum, q.alpha, q.psum);
   };
-  auto sm_cvt = [&](const f32x16& s, bf16x8* pb) {
+  auto sm_cvt = [&](const f32x16& s, u32x4* pb) {
     float pv[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) pv[e] = s[e];
-    pb[0] = to_bf16x8(pv);
+    pb[0] = pack8<T>(pv);
 #pragma unroll
     for (int e = 0; e < 8; ++e) pv[e] = s[8 + e];
-    pb[1] = to_bf16x8(pv);
+    pb[1] = pack8<T>(pv);
   };
   // Logical softmax piece p (0..7) of a half: max (dense) or prep (paged),
   // 4 x exp, convert, sum.
-  auto sm_piece = [&](int p, f32x16& s, int k0, bool mask, Soft& q, bf16x8* pb, bool first) {
+  auto sm_piece = [&](int p, f32x16& s, int k0, bool mask, Soft& q, u32x4* pb, bool first) {
     if (p == 0) {
       if (kFast) fs_prep(s, k0, mask, first);
       else sm_max(s, k0, mask, q);
@@ -863,7 +862,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   // the branch, in the region where they overlap the MFMAs).  Paged: the rare
   // fix-up of a half whose p passed 2^T (S recomputed from the stage `st`,
   // half kb), then the half's sum joins the row's.
-  auto commit = [&](Soft& q, const char* st, int kb, int k0, bool mask, bf16x8* pb) {
+  auto commit = [&](Soft& q, const char* st, int kb, int k0, bool mask, u32x4* pb) {
     if (!kFast) {
       if (__builtin_amdgcn_ballot_w64(q.alpha != 1.f || q.psum < 0.f)) {
 #pragma unroll
@@ -875,7 +874,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
       f32x16 t = {};
 #pragma unroll
       for (int kk = 0; kk < NQ; ++kk)
-        t = mfma32(as_bf16x8(*reinterpret_cast<const u32x4*>(st + 32 * kb * RW + koff[kk])), qB[kk], t);
+        t = E16<T>::mfma32(*reinterpret_cast<const u32x4*>(st + 32 * kb * RW + koff[kk]), qB[kk], t);
       const float nr = -rref;
 #pragma unroll
       for (int j = 0; j < 16; ++j) t[j] = __builtin_fmaf(t[j], sl2, nr);
@@ -890,7 +889,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 #pragma unroll
       for (int j = 0; j < 16; j += 2) {
         float e0 = fast_exp2(t[j] - d), e1 = fast_exp2(t[j + 1] - d);
-        round2_bf16(e0, e1);                    // the values the P V MFMA takes
+        round2<T>(e0, e1);                      // the values the P V MFMA takes
         t[j] = e0;
         t[j + 1] = e1;
       }
@@ -928,7 +927,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
                      bool first) {
     f32x16 s0, s1;
     u32x4 va0[2][NO], va1[2][NO];
-    bf16x8 pb0[2], pb1[2];
+    u32x4 pb0[2], pb1[2];
     Soft q0, q1;
     u32x4 ka[2][NQ];
 #pragma unroll
@@ -940,7 +939,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
     // after a barrier do not all hit LDS at once, and fewer registers are live
 #pragma unroll
     for (int kk = 0; kk < NQ; ++kk) {
-      s0 = mfma32(as_bf16x8(ka[0][kk]), qB[kk], s0);
+      s0 = E16<T>::mfma32(ka[0][kk], qB[kk], s0);
       ka[1][kk] = *reinterpret_cast<const u32x4*>(st + 32 * RW + koff[kk]);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -948,7 +947,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
     constexpr int V_PER = 2 * NO / NQ;           // V operand reads (pairs) per slot
 #pragma unroll
     for (int kk = 0; kk < NQ; ++kk) {
-      s1 = mfma32(as_bf16x8(ka[1][kk]), qB[kk], s1);
+      s1 = E16<T>::mfma32(ka[1][kk], qB[kk], s1);
 #pragma unroll
       for (int v = 0; v < V_PER; ++v) {
         const int idx = kk * V_PER + v;          // (tp, db) = (idx / NO, idx % NO)
@@ -964,7 +963,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 #pragma unroll
     for (int i = 0; i < 2 * NO; ++i) {
       const int tp = i / NO, db = i % NO;
-      o[db] = mfma32(as_bf16x8(va0[tp][db]), pb0[tp], o[db]);
+      o[db] = E16<T>::mfma32(va0[tp][db], pb0[tp], o[db]);
       va1[tp][db] = vread1(st, 1, tp, db);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -980,7 +979,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 #pragma unroll
       for (int i = 0; i < 2 * NO; ++i) {
         const int tp = i / NO, db = i % NO;
-        o[db] = mfma32(as_bf16x8(va1[tp][db]), pb1[tp], o[db]);
+        o[db] = E16<T>::mfma32(va1[tp][db], pb1[tp], o[db]);
         if (i < 2 * CHD) {
           if (KV8)
             fp8_put(dstage, i / 2, i % 2);     // fetched at the start of the tile
@@ -993,7 +992,7 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 #pragma unroll
       for (int i = 0; i < 2 * NO; ++i) {
         const int tp = i / NO, db = i % NO;
-        o[db] = mfma32(as_bf16x8(va1[tp][db]), pb1[tp], o[db]);
+        o[db] = E16<T>::mfma32(va1[tp][db], pb1[tp], o[db]);
       }
     }
   };
@@ -1050,18 +1049,18 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
   {
     float x[NQ][8];
 #pragma unroll
-    for (int kk = 0; kk < NQ; ++kk) unpack_bf16x8(qraw[kk], x[kk]);
+    for (int kk = 0; kk < NQ; ++kk) unpack8<T>(qraw[kk], x[kk]);
     if (q_rope) {
 #pragma unroll
       for (int kk = 0; kk < NQ / 2; ++kk) {
         float c[8], sn[8];
-        unpack_bf16x8(craw[kk], c);
-        unpack_bf16x8(sraw[kk], sn);
-        rope8_bf16(x[kk], x[kk + NQ / 2], c, sn);
+        unpack8<T>(craw[kk], c);
+        unpack8<T>(sraw[kk], sn);
+        rope8<T>(x[kk], x[kk + NQ / 2], c, sn);
       }
     }
 #pragma unroll
-    for (int kk = 0; kk < NQ; ++kk) qB[kk] = to_bf16x8(x[kk]);   // exact: q and its rotation are bf16
+    for (int kk = 0; kk < NQ; ++kk) qB[kk] = pack8<T>(x[kk]);   // exact: q and its rotation are in T
   }
   if (!DENSE) __syncthreads();  // block ids in LDS visible
   if (TPB < ntiles) dma_bids(TPB * BN, nbid);
@@ -1098,13 +1097,13 @@ __device__ __forceinline__ void prefill_wg(const AttnArgs& a, const WorkItem& it
 
   if (row_ok) {
     const float inv = 1.f / sum_xor32(lsum);
-    __bf16* op = (__bf16*)a.out + qrow * a.out_row_stride + (int64_t)qh * D + 4 * h;
+    T* op = (T*)a.out + qrow * a.out_row_stride + (int64_t)qh * D + 4 * h;
 #pragma unroll
     for (int db = 0; db < NO; ++db)
 #pragma unroll
       for (int jq = 0; jq < 4; ++jq) {
-        u32x2 w = {pack_bf16x2(o[db][4 * jq] * inv, o[db][4 * jq + 1] * inv),
-                   pack_bf16x2(o[db][4 * jq + 2] * inv, o[db][4 * jq + 3] * inv)};
+        u32x2 w = {E16<T>::pack2(o[db][4 * jq] * inv, o[db][4 * jq + 1] * inv),
+                   E16<T>::pack2(o[db][4 * jq + 2] * inv, o[db][4 * jq + 3] * inv)};
         st8(op + 32 * db + 8 * jq, w);
       }
   }
@@ -1136,22 +1135,23 @@ __device__ __forceinline__ int xcd_item(int b, int n) {
 }
 
 // Work items of both kinds in one launch (mixed continuous batch; 8-wave
-// workgroups), or decode items only (HW x KW waves).
-template <int D, bool PF, bool DC, int HW, int KW, bool KV8>
-__global__ void __launch_bounds__(64 * HW * KW) paged_attn_bf16_kernel(AttnArgs a) {
+// workgroups), or decode items only (HW x KW waves).  T: the model dtype
+// (__bf16 or _Float16), also the cache's unless KV8 (fp8 e4m3fn cache).
+template <typename T, int D, bool PF, bool DC, int HW, int KW, bool KV8>
+__global__ void __launch_bounds__(64 * HW * KW) paged_attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[MixedLds<D, PF, DC, HW * KW>::kBytes];
   const WorkItem it = a.items[xcd_item<!PF && KV8 && HW * D < 128>(blockIdx.x, a.n_items)];
   if (PF && (!DC || (it.kind_b & 0xff) == kItemPrefill)) {
     if constexpr (HW * KW == kWaves)
-      prefill_wg<D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
+      prefill_wg<T, D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
     return;
   }
-  if constexpr (DC) decode_wg<D, HW, KW, KV8>(a, it, lds);
+  if constexpr (DC) decode_wg<T, D, HW, KW, KV8>(a, it, lds);
 }
 
 // Page-balanced decode: workgroup w runs its key segments in order (all
 // waves converge between segments; the LDS staging is reused).
-template <int D, int HW, int KW, bool KV8>
+template <typename T, int D, int HW, int KW, bool KV8>
 __global__ void __launch_bounds__(64 * HW * KW) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4 : 2)))
 decode_balanced_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[DecodeCfg<D, HW * KW>::kLdsBytes];
@@ -1162,7 +1162,7 @@ decode_balanced_kernel(AttnArgs a) {
     const DecodeSeg sg = a.segs[s];
     const DecodeTask tk{sg.seq, sg.hg, sg.k0, sg.k1, sg.q_row_start, sg.ctx_len, sg.q_len,
                         sg.nseg, sg.pbase, sg.ord, sg.ticket};
-    decode_task<D, HW, KW, KV8>(a, tk, lds, &ticket);
+    decode_task<T, D, HW, KW, KV8>(a, tk, lds, &ticket);
   }
 }
 
@@ -1170,14 +1170,14 @@ decode_balanced_kernel(AttnArgs a) {
 // key shares of the decode sequences (segments, as decode_balanced_kernel);
 // each later workgroup runs one prefill item.  One 8-wave workgroup per CU
 // (the prefill path's LDS ring and registers).
-template <int D, int HW, bool KV8>
+template <typename T, int D, int HW, bool KV8>
 __global__ void __launch_bounds__(64 * kWaves) mixed_balanced_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[MixedLds<D, true, true, kWaves>::kBytes];
   __shared__ int ticket;
   const int b = blockIdx.x;
   if (b >= a.n_seg_wgs) {
     const WorkItem it = a.items[b - a.n_seg_wgs];
-    prefill_wg<D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
+    prefill_wg<T, D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
     return;
   }
   const int s0 = a.seg_ptr[b], s1 = a.seg_ptr[b + 1];
@@ -1186,86 +1186,86 @@ __global__ void __launch_bounds__(64 * kWaves) mixed_balanced_kernel(AttnArgs a)
     const DecodeSeg sg = a.segs[s];
     const DecodeTask tk{sg.seq, sg.hg, sg.k0, sg.k1, sg.q_row_start, sg.ctx_len, sg.q_len,
                         sg.nseg, sg.pbase, sg.ord, sg.ticket};
-    decode_task<D, HW, kWaves / HW, KV8>(a, tk, lds, &ticket);
+    decode_task<T, D, HW, kWaves / HW, KV8>(a, tk, lds, &ticket);
   }
 }
 
 // Prefill items only: one 8-wave workgroup per CU, a 4-stage ring.
-template <int D, bool KV8>
+template <typename T, int D, bool KV8>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2)))
-prefill_bf16_kernel(AttnArgs a) {
+prefill_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[PrefillCfg<D, kPrefillStages>::kLdsBytes];
   const WorkItem it = a.items[blockIdx.x];
-  prefill_wg<D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
+  prefill_wg<T, D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
 }
 
-template <int D>
-__global__ void __launch_bounds__(64 * kWaves) dense_attn_bf16_kernel(AttnArgs a, int nwg) {
+template <typename T, int D>
+__global__ void __launch_bounds__(64 * kWaves) dense_attn_kernel(AttnArgs a, int nwg) {
   __shared__ __attribute__((aligned(16))) char lds[PrefillCfg<D, kPrefillStages>::kLdsBytes];
   const int w = blockIdx.x % nwg;
   const int rest = blockIdx.x / nwg;
   const int kvh = rest % a.num_kv_heads;
   const int b = rest / a.num_kv_heads;
   const WorkItem none{};
-  prefill_wg<D, true, kWaves, kPrefillStages, false>(a, none, b, kvh, w, lds);
+  prefill_wg<T, D, true, kWaves, kPrefillStages, false>(a, none, b, kvh, w, lds);
 }
 
-template <int D, int HW, int KW, bool KV8>
+template <typename T, int D, int HW, int KW, bool KV8>
 static void launch_paged_hk(const AttnArgs& a, bool pf, bool dc, hipStream_t st) {
   dim3 grid(a.n_items);
   if (pf && dc) {
     if constexpr (HW * KW == kWaves)
-      hipLaunchKernelGGL((paged_attn_bf16_kernel<D, true, true, HW, KW, KV8>), grid, dim3(64 * kWaves), 0, st, a);
+      hipLaunchKernelGGL((paged_attn_kernel<T, D, true, true, HW, KW, KV8>), grid, dim3(64 * kWaves), 0, st, a);
   } else if (pf) {
-    hipLaunchKernelGGL((prefill_bf16_kernel<D, KV8>), grid, dim3(64 * kWaves), 0, st, a);
+    hipLaunchKernelGGL((prefill_kernel<T, D, KV8>), grid, dim3(64 * kWaves), 0, st, a);
   } else {
-    hipLaunchKernelGGL((paged_attn_bf16_kernel<D, false, true, HW, KW, KV8>), grid, dim3(64 * HW * KW), 0, st, a);
+    hipLaunchKernelGGL((paged_attn_kernel<T, D, false, true, HW, KW, KV8>), grid, dim3(64 * HW * KW), 0, st, a);
   }
 }
 
-template <int D, bool KV8>
+template <typename T, int D, bool KV8>
 static hipError_t launch_decode_balanced(const AttnArgs& a, hipStream_t st) {
   const dim3 grid(a.n_items);
   switch (a.heads_per_wg) {
-    case 1: hipLaunchKernelGGL((decode_balanced_kernel<D, 1, 8, KV8>), grid, dim3(512), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((decode_balanced_kernel<D, 2, 4, KV8>), grid, dim3(512), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((decode_balanced_kernel<D, 4, 2, KV8>), grid, dim3(512), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((decode_balanced_kernel<D, 8, 1, KV8>), grid, dim3(512), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((decode_balanced_kernel<T, D, 1, 8, KV8>), grid, dim3(512), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((decode_balanced_kernel<T, D, 2, 4, KV8>), grid, dim3(512), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((decode_balanced_kernel<T, D, 4, 2, KV8>), grid, dim3(512), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((decode_balanced_kernel<T, D, 8, 1, KV8>), grid, dim3(512), 0, st, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
-template <int D, bool KV8>
+template <typename T, int D, bool KV8>
 static hipError_t launch_mixed_balanced(const AttnArgs& a, hipStream_t st) {
   const dim3 grid(a.n_items);
   switch (a.heads_per_wg) {
-    case 1: hipLaunchKernelGGL((mixed_balanced_kernel<D, 1, KV8>), grid, dim3(64 * kWaves), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((mixed_balanced_kernel<D, 2, KV8>), grid, dim3(64 * kWaves), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((mixed_balanced_kernel<D, 4, KV8>), grid, dim3(64 * kWaves), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((mixed_balanced_kernel<D, 8, KV8>), grid, dim3(64 * kWaves), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((mixed_balanced_kernel<T, D, 1, KV8>), grid, dim3(64 * kWaves), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((mixed_balanced_kernel<T, D, 2, KV8>), grid, dim3(64 * kWaves), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((mixed_balanced_kernel<T, D, 4, KV8>), grid, dim3(64 * kWaves), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((mixed_balanced_kernel<T, D, 8, KV8>), grid, dim3(64 * kWaves), 0, st, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
-template <int D, bool KV8>
+template <typename T, int D, bool KV8>
 static hipError_t launch_paged_d(const AttnArgs& a, bool pf, bool dc, hipStream_t st) {
   const int hw = a.heads_per_wg, nw = a.decode_waves;
   if (a.n_segs > 0) {
     if (nw != kWaves || (pf && a.prefill_waves != kWaves) || a.n_seg_wgs <= 0 || a.n_seg_wgs > a.n_items)
       return hipErrorInvalidValue;
-    if (pf) return dc ? launch_mixed_balanced<D, KV8>(a, st) : hipErrorInvalidValue;
-    return launch_decode_balanced<D, KV8>(a, st);
+    if (pf) return dc ? launch_mixed_balanced<T, D, KV8>(a, st) : hipErrorInvalidValue;
+    return launch_decode_balanced<T, D, KV8>(a, st);
   }
   if (pf && (a.prefill_waves != kWaves || (dc && nw != kWaves)))
     return hipErrorInvalidValue;
   if (nw == 8) {
     switch (hw) {
-      case 1: launch_paged_hk<D, 1, 8, KV8>(a, pf, dc, st); break;
-      case 2: launch_paged_hk<D, 2, 4, KV8>(a, pf, dc, st); break;
-      case 4: launch_paged_hk<D, 4, 2, KV8>(a, pf, dc, st); break;
-      case 8: launch_paged_hk<D, 8, 1, KV8>(a, pf, dc, st); break;
+      case 1: launch_paged_hk<T, D, 1, 8, KV8>(a, pf, dc, st); break;
+      case 2: launch_paged_hk<T, D, 2, 4, KV8>(a, pf, dc, st); break;
+      case 4: launch_paged_hk<T, D, 4, 2, KV8>(a, pf, dc, st); break;
+      case 8: launch_paged_hk<T, D, 8, 1, KV8>(a, pf, dc, st); break;
       default: return hipErrorInvalidValue;
     }
   } else {
@@ -1273,35 +1273,63 @@ static hipError_t launch_paged_d(const AttnArgs& a, bool pf, bool dc, hipStream_
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !dc || a.n_partials == 0) return e;
-  hipLaunchKernelGGL((merge_splits_kernel<D>), dim3(a.num_seqs * a.num_kv_heads), dim3(64), 0, st, a);
+  hipLaunchKernelGGL((merge_splits_kernel<T, D>), dim3(a.num_seqs * a.num_kv_heads), dim3(64), 0, st, a);
   return hipGetLastError();
 }
 
-hipError_t launch_paged_attention_bf16(const AttnArgs& a, bool has_prefill, bool has_decode, hipStream_t st) {
-  if (a.n_items == 0) return hipSuccess;
+template <typename T>
+static hipError_t launch_paged_t(const AttnArgs& a, bool pf, bool dc, hipStream_t st) {
   const bool kv8 = a.kv_dtype == kFP8;
-  if (!kv8 && a.kv_dtype != kBF16) return hipErrorInvalidValue;
-  if (a.head_dim == 64)
-    return kv8 ? launch_paged_d<64, true>(a, has_prefill, has_decode, st) : launch_paged_d<64, false>(a, has_prefill, has_decode, st);
+  if (a.head_dim == 64) return kv8 ? launch_paged_d<T, 64, true>(a, pf, dc, st) : launch_paged_d<T, 64, false>(a, pf, dc, st);
   if (a.head_dim == 128)
-    return kv8 ? launch_paged_d<128, true>(a, has_prefill, has_decode, st) : launch_paged_d<128, false>(a, has_prefill, has_decode, st);
+    return kv8 ? launch_paged_d<T, 128, true>(a, pf, dc, st) : launch_paged_d<T, 128, false>(a, pf, dc, st);
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_dense_attention_bf16(const AttnArgs& a, int B, int Tq, hipStream_t st) {
+template <typename T>
+static hipError_t launch_dense_t(const AttnArgs& a, dim3 grid, int nwg, hipStream_t st) {
+  const dim3 block(64 * kWaves);
+  if (a.head_dim == 64)
+    hipLaunchKernelGGL((dense_attn_kernel<T, 64>), grid, block, 0, st, a, nwg);
+  else if (a.head_dim == 128)
+    hipLaunchKernelGGL((dense_attn_kernel<T, 128>), grid, block, 0, st, a, nwg);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+#ifdef GLLM_PAGED_F16
+// fp16 models: this file compiled a second time (paged_attention_f16.hip), so
+// the two element types build as separate units in parallel.
+hipError_t launch_paged_f16(const AttnArgs& a, bool pf, bool dc, hipStream_t st) {
+  return launch_paged_t<_Float16>(a, pf, dc, st);
+}
+hipError_t launch_dense_f16(const AttnArgs& a, dim3 grid, int nwg, hipStream_t st) {
+  return launch_dense_t<_Float16>(a, grid, nwg, st);
+}
+#else
+hipError_t launch_paged_f16(const AttnArgs& a, bool pf, bool dc, hipStream_t st);
+hipError_t launch_dense_f16(const AttnArgs& a, dim3 grid, int nwg, hipStream_t st);
+
+hipError_t launch_paged_attention_mfma(const AttnArgs& a, bool has_prefill, bool has_decode, hipStream_t st) {
+  if (a.n_items == 0) return hipSuccess;
+  // the cache holds the model dtype or fp8 e4m3fn
+  if (a.kv_dtype != kFP8 && a.kv_dtype != a.dtype) return hipErrorInvalidValue;
+  if (a.dtype == kBF16) return launch_paged_t<__bf16>(a, has_prefill, has_decode, st);
+  if (a.dtype == kF16) return launch_paged_f16(a, has_prefill, has_decode, st);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_dense_attention_mfma(const AttnArgs& a, int B, int Tq, hipStream_t st) {
   const int G = a.num_q_heads / a.num_kv_heads;
   const int nwg = (G * ((Tq + 31) / 32) + kWaves - 1) / kWaves;
   const int64_t blocks = (int64_t)B * a.num_kv_heads * nwg;
   if (blocks == 0) return hipSuccess;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  dim3 grid((unsigned)blocks), block(64 * kWaves);
-  if (a.head_dim == 64)
-    hipLaunchKernelGGL((dense_attn_bf16_kernel<64>), grid, block, 0, st, a, nwg);
-  else if (a.head_dim == 128)
-    hipLaunchKernelGGL((dense_attn_bf16_kernel<128>), grid, block, 0, st, a, nwg);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  const dim3 grid((unsigned)blocks);
+  if (a.dtype == kBF16) return launch_dense_t<__bf16>(a, grid, nwg, st);
+  if (a.dtype == kF16) return launch_dense_f16(a, grid, nwg, st);
+  return hipErrorInvalidValue;
 }
 
 __global__ void fill_zero_i32_kernel(int32_t* p, int64_t n) {
@@ -1315,5 +1343,6 @@ hipError_t launch_fill_zero_i32(int32_t* p, int64_t n, hipStream_t st) {
   hipLaunchKernelGGL(fill_zero_i32_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p, n);
   return hipGetLastError();
 }
+#endif  // GLLM_PAGED_F16
 
 }  // namespace gllm

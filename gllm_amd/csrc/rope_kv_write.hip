@@ -1,5 +1,6 @@
-// Fused rotate-half RoPE + paged KV-cache write (cache in the model dtype,
-// bf16 under an fp32 model, or fp8 e4m3fn).
+// Fused rotate-half RoPE + paged KV-cache write.  Model dtype f32, bf16 or
+// f16; cache f32, bf16, f16 or fp8 e4m3fn, in any pairing (each written value
+// cast like torch's .to(kv_dtype)).
 //
 // Replaces gllm/model/layers/attention.py:151-161 (apply_rope on k, the
 // index_put_ of k/v through query_slot_mapping) and, optionally, the q half
@@ -33,6 +34,12 @@ template <> struct Elem<__bf16> {
   // the same with every op rounded to bf16 (RNE), like torch's bf16 ops
   __device__ static void rope(float& x1, float& x2, float c, float s) { rope_pair_bf16(x1, x2, c, s); }
 };
+template <> struct Elem<_Float16> {
+  static constexpr int kVec = 8;
+  __device__ static void load(const void* p, float* v) { unpack8<_Float16>(ld16(p), v); }
+  // every op rounded to fp16 (RNE), like torch's fp16 ops
+  __device__ static void rope(float& x1, float& x2, float c, float s) { rope_pair<_Float16>(x1, x2, c, s); }
+};
 
 // Store `n` values (already representable in T when T is the model dtype)
 // as element type S at p.
@@ -56,6 +63,14 @@ template <> __device__ void store_vals<__bf16>(void* p, const float* v, int n) {
     u32x2 w;
     for (int i = 0; i < 2; ++i) w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
     st8(p, w);
+  }
+}
+
+template <> __device__ void store_vals<_Float16>(void* p, const float* v, int n) {
+  if (n == 8) {
+    st16(p, pack8<_Float16>(v));
+  } else {  // n == 4
+    st8(p, u32x2{E16<_Float16>::pack2(v[0], v[1]), E16<_Float16>::pack2(v[2], v[3])});
   }
 }
 
@@ -147,6 +162,20 @@ __global__ void __launch_bounds__(256) rope_kv_write_kernel(RopeKVWriteArgs a) {
   }
 }
 
+// Model dtype T; the cache's from a.kv_dtype (q-only calls carry no cache).
+template <typename T>
+static hipError_t launch_rope_kv_t(const RopeKVWriteArgs& a, dim3 grid, hipStream_t stream) {
+  const dim3 block(256);
+  switch (a.k ? a.kv_dtype : a.dtype) {
+    case kF32: hipLaunchKernelGGL((rope_kv_write_kernel<T, float>), grid, block, 0, stream, a); break;
+    case kBF16: hipLaunchKernelGGL((rope_kv_write_kernel<T, __bf16>), grid, block, 0, stream, a); break;
+    case kF16: hipLaunchKernelGGL((rope_kv_write_kernel<T, _Float16>), grid, block, 0, stream, a); break;
+    case kFP8: hipLaunchKernelGGL((rope_kv_write_kernel<T, fp8e4m3>), grid, block, 0, stream, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_rope_kv_write(const RopeKVWriteArgs& a, hipStream_t stream) {
   const int V = a.dtype == kF32 ? 4 : 8;
   const int64_t per_tok = (a.k ? (int64_t)a.num_kv_heads * (a.head_dim / 2 / V + a.head_dim / V) : 0) +
@@ -154,20 +183,13 @@ hipError_t launch_rope_kv_write(const RopeKVWriteArgs& a, hipStream_t stream) {
   if (a.num_tokens * per_tok == 0) return hipSuccess;
   int64_t blocks = (a.num_tokens + 3) / 4;    // 4 waves of one token each
   if (blocks > 65536) blocks = 65536;
-  dim3 grid((unsigned)blocks), block(256);
-  if (a.dtype == kBF16 && a.kv_dtype == kBF16)
-    hipLaunchKernelGGL((rope_kv_write_kernel<__bf16, __bf16>), grid, block, 0, stream, a);
-  else if (a.dtype == kF32 && a.kv_dtype == kF32)
-    hipLaunchKernelGGL((rope_kv_write_kernel<float, float>), grid, block, 0, stream, a);
-  else if (a.dtype == kF32 && a.kv_dtype == kBF16)
-    hipLaunchKernelGGL((rope_kv_write_kernel<float, __bf16>), grid, block, 0, stream, a);
-  else if (a.dtype == kBF16 && a.kv_dtype == kFP8)
-    hipLaunchKernelGGL((rope_kv_write_kernel<__bf16, fp8e4m3>), grid, block, 0, stream, a);
-  else if (a.dtype == kF32 && a.kv_dtype == kFP8)
-    hipLaunchKernelGGL((rope_kv_write_kernel<float, fp8e4m3>), grid, block, 0, stream, a);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  const dim3 grid((unsigned)blocks);
+  switch (a.dtype) {
+    case kF32: return launch_rope_kv_t<float>(a, grid, stream);
+    case kBF16: return launch_rope_kv_t<__bf16>(a, grid, stream);
+    case kF16: return launch_rope_kv_t<_Float16>(a, grid, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace gllm

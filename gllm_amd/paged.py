@@ -115,7 +115,8 @@ def qkv_rope_kv_write(x: torch.Tensor, w_q: torch.Tensor | None, w_k: torch.Tens
     ``unfused_from``: from this many tokens the projections run as three
     ``F.linear`` (hipBLASLt) followed by :func:`rope_kv_write`, which is faster
     there; None runs the fused kernel at any size.  Head dims other than 64
-    and 128 always take the unfused path.
+    and 128, and models that are not bf16 (the fused kernel's projection is
+    bf16 MFMA), always take the unfused path.
     """
     hidden = x.shape[-1]
     xs = x.reshape(-1, hidden)
@@ -161,7 +162,7 @@ def qkv_rope_kv_write(x: torch.Tensor, w_q: torch.Tensor | None, w_k: torch.Tens
     rr = None
     if rope_rows is not None:
         rr = rope_rows.reshape(-1).to(torch.int64).contiguous()
-    if (unfused_from is not None and n >= unfused_from) or D not in (64, 128):   # the fused kernel: D 64 / 128
+    if (unfused_from is not None and n >= unfused_from) or D not in (64, 128) or x.dtype != torch.bfloat16:
         k = F.linear(xs, w_k).view(n, Hkv, D)
         v = F.linear(xs, w_v).view(n, Hkv, D)
         q = F.linear(xs, w_q).view(n, Hq, D) if w_q is not None else None

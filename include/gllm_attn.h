@@ -50,7 +50,12 @@ enum {
   GLLM_ATTN_EHIP = 3          /* HIP runtime error */
 };
 
-enum { GLLM_DTYPE_F32 = 0, GLLM_DTYPE_BF16 = 1, GLLM_DTYPE_FP8_E4M3 = 2 /* torch.float8_e4m3fn, KV cache only */ };
+enum {
+  GLLM_DTYPE_F32 = 0,
+  GLLM_DTYPE_BF16 = 1,
+  GLLM_DTYPE_FP8_E4M3 = 2, /* torch.float8_e4m3fn, KV cache only */
+  GLLM_DTYPE_F16 = 3
+};
 
 enum {
   GLLM_ROPE_NONE = 0,        /* q already rotated */
@@ -162,9 +167,11 @@ int gllm_qkv_rope_kv_write_noalloc(const void* x, int64_t x_row_stride, int64_t 
  * written for them (their q_out rows included) and their cos/sin rows are
  * not read.  Slots outside
  * [0, num_slots) are never written.  cos/sin rows: rope_rows[t] if given,
- * else t.  dtype is the model dtype of q/k/v/cos/sin; kv_dtype the cache's
- * (the model dtype, bf16 under f32, or fp8 e4m3fn: rounded like torch's
- * .to(torch.float8_e4m3fn), NaN -> 0x7f|sign, |x| > 464 -> NaN).
+ * else t.  dtype is the model dtype of q/k/v/cos/sin (f32, bf16 or f16);
+ * kv_dtype the cache's (f32, bf16, f16 or fp8 e4m3fn, any pairing, as
+ * model.py:64,75 allow): each written value is cast like torch's
+ * .to(kv_dtype) (round to nearest even; fp8: NaN -> 0x7f|sign,
+ * |x| > 464 -> NaN).
  * Every op is rounded to the model dtype in the reference's order, so the
  * written K/V are bit-identical to attention.py:151-161.  With k == v == NULL
  * only q is rotated into q_out (Attention.apply_rope on one tensor).
@@ -227,11 +234,13 @@ int gllm_attn_plan_destroy(gllm_attn_plan* plan);
  * Key p of sequence i is visible to query row r iff p <= c_i + r.
  * Query head h reads kv head h / (num_q_heads / num_kv_heads).
  * rope_mode != NONE rotates q on load (bit-identical to apply_rope).
- * bf16 model dtype runs the MFMA kernels (head_dim 64 or 128) over a bf16 or
- * fp8 e4m3fn cache, and a generic kernel (fp32 arithmetic, bf16 in and out)
- * for any other even head_dim up to 256; f32 model dtype runs the generic
- * kernel (kv f32, bf16 or fp8 e4m3fn).  An fp8 cache is read as the reference reads it: each value
- * widened exactly to the model dtype (attention.py:169-170's .to(q.dtype)).
+ * A bf16 or f16 model dtype runs the MFMA kernels (head_dim 64 or 128) over
+ * a cache in the model dtype or fp8 e4m3fn; every other pairing (f32 model;
+ * a 16-bit model over an f32 or the other 16-bit cache; other even head dims
+ * up to 256) runs a generic kernel (fp32 arithmetic, model dtype in and
+ * out).  Cached values are read as the reference reads them: cast to the
+ * model dtype (attention.py:169-170's .to(q.dtype); exact for fp8, rounded
+ * to nearest even where the cache is wider).
  * Returns after enqueueing on `stream`.
  */
 int gllm_paged_attention(const gllm_attn_plan* plan, const void* q, int64_t q_row_stride,
@@ -246,8 +255,9 @@ int gllm_paged_attention(const gllm_attn_plan* plan, const void* q, int64_t q_ro
  * reference_attention(q, k, v, bias): softmax(q k^T * scale + bias) v with
  * GQA.  q/out [B, T_q, Hq, D] (row stride q_row_stride, batch = T_q rows),
  * k/v [B, T, Hkv, D] with the given batch / row strides, bias [B, T_q, T]
- * (model dtype) with batch / row strides, last dim contiguous.  A row whose
- * bias is -inf everywhere comes out NaN, as torch's softmax makes it.
+ * (model dtype: f32, bf16 or f16) with batch / row strides, last dim
+ * contiguous.  A row whose bias is -inf everywhere comes out NaN, as torch's
+ * softmax makes it.
  */
 int gllm_attention_dense(const void* q, int64_t q_row_stride, const void* k, int64_t k_batch_stride,
                          int64_t k_row_stride, const void* v, int64_t v_batch_stride,

@@ -94,7 +94,9 @@ def paged_attention(q_rows: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.
     ``p <= c_i + r`` (the 0/-inf pattern ``llm.py:264-274`` builds, on real
     rows).  ``q_rows`` is ``[rows, Hq, D]`` with sequence ``i``'s rows at
     ``q_row_start[i] .. + q_i``.  Returns ``[rows, Hq, D]`` in ``dtype``;
-    rows not owned by any sequence are left zero.
+    rows not owned by any sequence are left zero.  Cached K/V are read as
+    the reference's gather reads them, cast to the model dtype (``q_rows``'
+    dtype, ``attention.py:169-170``), and only then widened to ``dtype``.
     """
     Hq, D = q_rows.shape[-2], q_rows.shape[-1]
     Hkv = k_cache.shape[-2]
@@ -107,8 +109,8 @@ def paged_attention(q_rows: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.
             continue
         p = torch.arange(L)
         slots = block_table[i, p // block_size].to(torch.int64) * block_size + p % block_size
-        kk = k_cache[slots].to(dtype)               # [L, Hkv, D]
-        vv = v_cache[slots].to(dtype)
+        kk = k_cache[slots].to(q_rows.dtype).to(dtype)   # [L, Hkv, D]; the gather's cast, then fp32
+        vv = v_cache[slots].to(q_rows.dtype).to(dtype)
         qq = q_rows[r0:r0 + qn].to(dtype)           # [qn, Hq, D]
         kk = torch.repeat_interleave(kk, G, dim=1)  # head h -> kv head h // G
         vv = torch.repeat_interleave(vv, G, dim=1)

@@ -399,7 +399,7 @@ def test_fp32_paged_long_contexts(D, kv):
                                              (1, 256, 256, 1, 1, 128), (1, 32, 256, 1, 1, 128),
                                              (1, 32, 256, 2, 1, 128), (8, 32, 256, 1, 1, 128),
                                              (3, 5, 77, 32, 8, 64)])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_dense_op_reference_shapes(B, Tq, T, Hq, Hkv, D, dtype):
     """The reference's own op-test shapes (tests/test_attention_op.py:12-34),
     causal-with-offset bias (:56-61), seeded."""
@@ -420,7 +420,7 @@ def test_dense_op_reference_shapes(B, Tq, T, Hq, Hkv, D, dtype):
         assert_close_bf16(out, ref, "dense bf16")
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_dense_op_engine_bias_and_masked_rows(dtype):
     """Left-padded engine bias (llm.py:259-274) and a fully masked row (NaN,
     as torch's softmax)."""
@@ -476,7 +476,7 @@ def test_dense_op_random_bias(k):
 
 
 # ------------------------------------------------------------ call-site drop-in
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_attention_forward_dropin(dtype):
     """gllm_amd.Attention.attention == attention.py:151-178 (oracle) on real
     rows; cache contents bit-exact outside the dummy block."""
@@ -516,7 +516,7 @@ def test_attention_forward_dropin(dtype):
             assert_close_bf16(out[i, :ql[i]], ref[i, :ql[i]], f"drop-in seq {i}")
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_attention_layer_forward_real_weights(dtype):
     """gllm_amd.Attention.forward (projections, RoPE, KV write, attention,
     linear_o) == attention.py:122-182 restated by the oracle, on random

@@ -447,3 +447,57 @@ def test_silu_mlp_properties():
     assert torch.allclose(oe.mlp(xr, lw3), 2.5 * oe.mlp(xr, lw2), atol=1e-12)
     assert torch.equal(oe.mlp(xr, dict(lw2, up=torch.zeros(8, 8, dtype=torch.float64))),
                        torch.zeros(3, 8, dtype=torch.float64))
+
+
+def test_apply_rope_fp16_rounds_after_every_op():
+    """attention.py:105-118 for an fp16 model: six torch ops, each rounded to
+    fp16.  numpy float16 arithmetic (each op evaluated in float32 and rounded
+    to float16, as torch's CPU half ops do) reproduces the oracle bit for
+    bit; rounding only the exact result once differs often enough to tell
+    the two apart."""
+    g = torch.Generator().manual_seed(19)
+    D = 64
+    x = (torch.randn(3, 50, 2, D, generator=g) * 3).to(torch.float16)
+    cos_t, sin_t = orope.rope_cache(4096, D, 500000.0, torch.float16)
+    pos = torch.randint(0, 4096, (3, 50), generator=g)
+    c, s = cos_t[pos], sin_t[pos]
+    out = orope.apply_rope(x, c, s).numpy()
+    xf = x.numpy()
+    x1, x2 = xf[..., :D // 2], xf[..., D // 2:]
+    cf, sf = c.numpy()[:, :, None, :], s.numpy()[:, :, None, :]
+    want = np.concatenate([(x1 * cf) - (x2 * sf), (x1 * sf) + (x2 * cf)], axis=-1)
+    assert want.dtype == np.float16
+    assert np.array_equal(out.view(np.uint16), want.view(np.uint16))
+    x164, x264 = x1.astype(np.float64), x2.astype(np.float64)
+    c64, s64 = cf.astype(np.float64), sf.astype(np.float64)
+    once = np.concatenate([x164 * c64 - x264 * s64, x164 * s64 + x264 * c64], axis=-1).astype(np.float16)
+    assert (once != want).mean() > 0.05
+
+
+@pytest.mark.parametrize("model,cache", [(torch.bfloat16, torch.float32), (torch.float16, torch.float32),
+                                         (torch.bfloat16, torch.float16)])
+def test_paged_attention_casts_the_gather_to_the_model_dtype(model, cache):
+    """attention.py:169-170 gathers K/V with .to(q.dtype): a cache wider than
+    (or other than) the model dtype is rounded to the model dtype before the
+    attention.  The oracle's per-sequence form equals the reference's
+    call-site path (attention_layer_forward: write, gather, dense SDPA in
+    fp32) on such a cache, and the cast is visible: without it the result
+    differs."""
+    ctx, ql, bt, meta, kc, vc, q, k, v, cos, sin = _layer_case(3)
+    g = torch.Generator().manual_seed(33)
+    kc = torch.randn(kc.shape, generator=g).to(cache)
+    vc = torch.randn(vc.shape, generator=g).to(cache)
+    q, k, v = q.to(model), k.to(model), v.to(model)
+    cos, sin = cos.to(model), sin.to(model)
+    B, Tq = meta.query_slot_mapping.shape
+    out, qr, _ = oa.attention_layer_forward(q, k, v, cos, sin, kc, vc, meta, sdpa_dtype=torch.float32)
+    rows = qr.reshape(B * Tq, *qr.shape[2:])
+    po = oa.paged_attention(rows, kc, vc, torch.from_numpy(bt), ctx, ql, [i * Tq for i in range(B)], 4)
+    nocast = oa.paged_attention(rows.float(), kc.float(), vc.float(), torch.from_numpy(bt), ctx, ql,
+                                [i * Tq for i in range(B)], 4)
+    d_cast = d_nocast = 0.0
+    for i in range(B):
+        d_cast = max(d_cast, (po[i * Tq:i * Tq + ql[i]] - out[i, :ql[i]].float()).abs().max().item())
+        d_nocast = max(d_nocast, (nocast[i * Tq:i * Tq + ql[i]] - out[i, :ql[i]].float()).abs().max().item())
+    assert d_cast < 1e-5
+    assert d_nocast > 1e-4
