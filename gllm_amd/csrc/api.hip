@@ -306,8 +306,7 @@ struct PrefillPiece {
   int64_t kend;
   int64_t pairs;
 };
-void prefill_pieces(const SeqInfo& s, int i, int G, int Hkv, std::vector<PrefillPiece>& out) {
-  constexpr int pw = 8;
+void prefill_pieces(const SeqInfo& s, int i, int G, int Hkv, std::vector<PrefillPiece>& out, int pw = 8) {
   const int nrb = (s.q_len + 31) / 32;
   const int nwg = (G * nrb + pw - 1) / pw;
   for (int h = 0; h < Hkv; ++h)
@@ -734,7 +733,9 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
     p->heads_per_wg = best_hw;
     p->decode_waves = best_nw;
     // Prefill: 8-wave workgroups, one per CU (4-stage K/V ring in LDS).
-    const int pw = 8;
+    // prefill-only launches: kPrefillOnlyWaves-wave workgroups (prefill_kernel);
+    // a mixed launch's prefill items run in its 8-wave workgroups
+    const int pw = ndec == 0 ? kPrefillOnlyWaves : 8;
     p->prefill_waves = pw;
     const int hgroups = (num_kv_heads + best_hw - 1) / best_hw;
     const int64_t S = best_S;
@@ -764,7 +765,7 @@ int gllm_attn_plan_create(gllm_attn_plan** out, const int32_t* query_lens, const
       } else {
         ++p->n_prefill_seqs;
         pcs.clear();
-        prefill_pieces(s, i, G, num_kv_heads, pcs);
+        prefill_pieces(s, i, G, num_kv_heads, pcs, pw);
         for (const PrefillPiece& pc : pcs) pf.push_back({pc.kend, pc.it});
       }
     }

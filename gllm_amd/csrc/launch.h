@@ -32,6 +32,13 @@ struct RopeKVWriteArgs {
 
 enum : int32_t { kRopeNone = 0, kRopeByPosition = 1, kRopeByRow = 2 };
 
+// Prefill-only launches (prefill_kernel): waves per workgroup and LDS ring
+// stages, as in a mixed launch's prefill items.  Measured on config (c): two
+// 4-wave workgroups per CU with 2-stage rings (so one workgroup's start
+// overlaps the other's compute) 550-557 us against 516-518 us.
+constexpr int kPrefillOnlyWaves = 8;
+constexpr int kPrefillOnlyStages = 4;
+
 // Paged attention (decode / prefill / mixed) and the dense-bias op share it.
 struct AttnArgs {
   const void* q;             // query rows, heads at h*D within a row

@@ -1190,13 +1190,14 @@ __global__ void __launch_bounds__(64 * kWaves) mixed_balanced_kernel(AttnArgs a)
   }
 }
 
-// Prefill items only: one 8-wave workgroup per CU, a 4-stage ring.
+// Prefill items only: kPrefillOnlyWaves-wave workgroups with a
+// kPrefillOnlyStages-stage ring.
 template <typename T, int D, bool KV8>
-__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(64 * kPrefillOnlyWaves) __attribute__((amdgpu_waves_per_eu(2)))
 prefill_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) char lds[PrefillCfg<D, kPrefillStages>::kLdsBytes];
+  __shared__ __attribute__((aligned(16))) char lds[PrefillCfg<D, kPrefillOnlyStages>::kLdsBytes];
   const WorkItem it = a.items[blockIdx.x];
-  prefill_wg<T, D, false, kWaves, kPrefillStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
+  prefill_wg<T, D, false, kPrefillOnlyWaves, kPrefillOnlyStages, KV8>(a, it, it.seq, it.a, it.kind_b >> 8, lds);
 }
 
 template <typename T, int D>
@@ -1217,7 +1218,7 @@ static void launch_paged_hk(const AttnArgs& a, bool pf, bool dc, hipStream_t st)
     if constexpr (HW * KW == kWaves)
       hipLaunchKernelGGL((paged_attn_kernel<T, D, true, true, HW, KW, KV8>), grid, dim3(64 * kWaves), 0, st, a);
   } else if (pf) {
-    hipLaunchKernelGGL((prefill_kernel<T, D, KV8>), grid, dim3(64 * kWaves), 0, st, a);
+    hipLaunchKernelGGL((prefill_kernel<T, D, KV8>), grid, dim3(64 * kPrefillOnlyWaves), 0, st, a);
   } else {
     hipLaunchKernelGGL((paged_attn_kernel<T, D, false, true, HW, KW, KV8>), grid, dim3(64 * HW * KW), 0, st, a);
   }
@@ -1258,7 +1259,7 @@ static hipError_t launch_paged_d(const AttnArgs& a, bool pf, bool dc, hipStream_
     if (pf) return dc ? launch_mixed_balanced<T, D, KV8>(a, st) : hipErrorInvalidValue;
     return launch_decode_balanced<T, D, KV8>(a, st);
   }
-  if (pf && (a.prefill_waves != kWaves || (dc && nw != kWaves)))
+  if (pf && (a.prefill_waves != (dc ? kWaves : kPrefillOnlyWaves) || (dc && nw != kWaves)))
     return hipErrorInvalidValue;
   if (nw == 8) {
     switch (hw) {
