@@ -283,9 +283,11 @@ def bench_metadata(b: workloads.PagedBatch, warmup, reps, dev, cpu: bool):
 def bench_decode_step(dtype, warmup, reps, dev):
     """One decode step of a config (a)-shaped model's attention path (16
     layers of Llama-3.2-1B heads, 8 sequences, block size 16): per layer the
-    RoPE + KV write and the paged attention (``Attention.attention``), 32
-    launches.  Eager launches from Python vs the same step captured in one
-    HIP graph; returns both per-step times (median over ``reps``)."""
+    RoPE + KV write and the paged attention (``Attention.attention``: one
+    launch per layer that also writes the new K/V, or two where the fused
+    write does not apply).  Eager launches from Python vs the same step
+    captured in one HIP graph; returns both per-step times (median over
+    ``reps``)."""
     import gllm_amd
     L, Hq, Hkv, D, bs, B = 16, 32, 8, 64, 16, 8
     g = torch.Generator().manual_seed(31)
@@ -320,6 +322,8 @@ def bench_decode_step(dtype, warmup, reps, dev):
 
     step()                                         # builds the plan once
     torch.cuda.synchronize()
+    from gllm_amd import paged
+    fused = paged.fused_kv_write_ok(gm._gllm_plan, cache.physical_kv_cache.dtype)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -332,7 +336,8 @@ def bench_decode_step(dtype, warmup, reps, dev):
     eager = statistics.median(s_.elapsed_time(e_) for s_, e_ in ev)
     per, _ = graph_reps([step], warmup, reps, 1)
     graph = statistics.median(per)
-    return {"layers": L, "seqs": B, "dtype": str(dtype).replace("torch.", ""), "launches_per_step": 2 * L,
+    return {"layers": L, "seqs": B, "dtype": str(dtype).replace("torch.", ""), "launches_per_step": L if fused else 2 * L,
+            "kv_write_fused": fused,
             "eager_ms_per_step": eager, "graph_ms_per_step": graph, "saving_ms": eager - graph,
             "speedup": eager / graph}
 

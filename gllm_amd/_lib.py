@@ -38,6 +38,8 @@ SIGNATURES = {
     "gllm_attn_plan_destroy": (ctypes.c_int, [_p]),
     "gllm_paged_attention": (ctypes.c_int, [_p, _p, _i64, _p, _i64, _p, _p, _i64, _i64, _p, _i64, _p, _p,
                                             _i64, _i32, _f32, _i32, _i32, _p]),
+    "gllm_paged_attention_write_kv": (ctypes.c_int, [_p, _p, _i64, _p, _i64, _p, _p, _i64, _i64, _p, _i64, _p, _i64,
+                                                     _p, _i64, _p, _p, _i64, _i32, _f32, _i32, _i32, _p]),
     "gllm_build_metadata": (ctypes.c_int, [_p, _i64, _i64, _p, _p, _i32, _i64, _i32, _p, _p, _p, _i64, _p]),
     "gllm_qkv_rope_kv_write": (ctypes.c_int, [_p, _i64, _i64, _i32, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i32,
                                               _p, _p, _i64, _i64, _p, _p, _i64, _p, _p, _p, _i64, _i32, _i32, _i32,

@@ -139,11 +139,16 @@ class Attention:
         """The hot path between the projections and ``linear_o``
         (``attention.py:151-178``): returns ``[B, T_q, Hq, D]``."""
         k_cache, v_cache = kv_cache[0], kv_cache[1]
-        paged.rope_kv_write(k, v, cos_pos, sin_pos, k_cache, v_cache, meta.query_slot_mapping,
-                            query_lens=meta.query_lens)
         plan = plan_for(meta, num_q_heads=self.num_q_heads, num_kv_heads=self.num_kv_heads,
                         head_dim=self.head_dim, dtype=q.dtype, device=q.device,
                         block_size_hint=self._block_size)
         self._block_size = plan.block_size
+        if paged.fused_kv_write_ok(plan, k_cache.dtype):
+            # decode step: the RoPE + KV write inside the attention launch (one
+            # launch per layer); the slots are query_slot_mapping's, from the table
+            return paged.paged_attention(plan, q, k_cache, v_cache, meta.block_table,
+                                         rope=(cos_pos, sin_pos, "row"), kv_new=(k, v))
+        paged.rope_kv_write(k, v, cos_pos, sin_pos, k_cache, v_cache, meta.query_slot_mapping,
+                            query_lens=meta.query_lens)
         return paged.paged_attention(plan, q, k_cache, v_cache, meta.block_table,
                                      rope=(cos_pos, sin_pos, "row"))

@@ -70,6 +70,9 @@ void block_div(int32_t bs, uint32_t* magic, int32_t* shift) {
   *shift = k;
 }
 constexpr int32_t kMaxBlockSize = 65536;
+// query rows per sequence up to which the generic kernel takes the fused KV
+// write (each workgroup stages the new keys it reads in LDS)
+constexpr int32_t kMaxFusedRows = 16;
 
 // Model dtypes (the reference's model_dtype, model.py:64): f32, bf16, f16;
 // cache dtypes (kv_dtype, model.py:75): those and fp8 e4m3fn, any pairing.
@@ -923,13 +926,14 @@ static int fill_common(AttnArgs& a, int32_t Hq, int32_t Hkv, int32_t D, float sc
   return ok();
 }
 
-int gllm_paged_attention(const gllm_attn_plan* p, const void* q, int64_t q_row_stride, void* out,
-                         int64_t out_row_stride, const void* k_cache, const void* v_cache,
-                         int64_t cache_slot_stride, int64_t num_blocks, const int32_t* block_table,
-                         int64_t block_table_stride, const void* rope_cos, const void* rope_sin,
-                         int64_t rope_row_stride, int32_t rope_mode, float scale, int32_t dtype,
-                         int32_t kv_dtype, void* stream) {
-  Range range("gllm_paged_attention");
+// gllm_paged_attention and, with k_new / v_new, gllm_paged_attention_write_kv.
+static int paged_attention_impl(const gllm_attn_plan* p, const void* q, int64_t q_row_stride, void* out,
+                                int64_t out_row_stride, const void* k_cache, const void* v_cache,
+                                int64_t cache_slot_stride, int64_t num_blocks, const int32_t* block_table,
+                                int64_t block_table_stride, const void* k_new, int64_t k_new_row_stride,
+                                const void* v_new, int64_t v_new_row_stride, const void* rope_cos,
+                                const void* rope_sin, int64_t rope_row_stride, int32_t rope_mode, float scale,
+                                int32_t dtype, int32_t kv_dtype, void* stream) {
   if (!p) return fail(GLLM_ATTN_EINVAL, "null plan");
   if (!p->ws) return fail(GLLM_ATTN_EINVAL, "plan was not uploaded (gllm_attn_plan_upload)");
   if (dtype != p->dtype) return fail(GLLM_ATTN_EINVAL, "dtype %d differs from the plan's %d", dtype, p->dtype);
@@ -973,14 +977,55 @@ int gllm_paged_attention(const gllm_attn_plan* p, const void* q, int64_t q_row_s
   a.heads_per_wg = p->heads_per_wg;
   a.decode_waves = p->decode_waves;
   a.prefill_waves = p->prefill_waves;
-  hipStream_t st = (hipStream_t)stream;
   // the MFMA kernels read a cache in the model dtype or fp8; a 16-bit model
   // over an f32 (or the other 16-bit) cache takes the generic kernel, which
   // rounds each cached value to the model dtype as the reference's gather does
-  if (p->mfma && (kv_dtype == dtype || kv_dtype == GLLM_DTYPE_FP8_E4M3))
+  const bool use_mfma = p->mfma && (kv_dtype == dtype || kv_dtype == GLLM_DTYPE_FP8_E4M3);
+  if (k_new || v_new) {
+    if (!k_new || !v_new) return fail(GLLM_ATTN_EINVAL, "k_new and v_new go together");
+    const int64_t kvd = (int64_t)p->Hkv * p->D;
+    if (k_new_row_stride < kvd || v_new_row_stride < kvd)
+      return fail(GLLM_ATTN_EINVAL, "k_new / v_new row stride < num_kv_heads * head_dim");
+    // every sequence on the decode path: its new keys are read only by the
+    // task that writes them (prefill items read other items' new keys)
+    if (use_mfma ? p->n_prefill_seqs > 0 : p->max_q > kMaxFusedRows)
+      return fail(GLLM_ATTN_EINVAL, "the fused KV write needs a decode-path plan (query_len x G <= 16 on the MFMA "
+                                    "kernels, query_len <= %d on the generic one)", kMaxFusedRows);
+    a.k_new = k_new; a.v_new = v_new;
+    a.k_new_row_stride = k_new_row_stride; a.v_new_row_stride = v_new_row_stride;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  if (use_mfma)
     return hip_check(launch_paged_attention_mfma(a, p->n_prefill_seqs > 0, p->n_decode_seqs > 0, st),
                      "paged attention launch");
   return hip_check(launch_attention_f32(a, false, p->num_seqs, p->max_q, st), "generic attention launch");
+}
+
+int gllm_paged_attention(const gllm_attn_plan* p, const void* q, int64_t q_row_stride, void* out,
+                         int64_t out_row_stride, const void* k_cache, const void* v_cache,
+                         int64_t cache_slot_stride, int64_t num_blocks, const int32_t* block_table,
+                         int64_t block_table_stride, const void* rope_cos, const void* rope_sin,
+                         int64_t rope_row_stride, int32_t rope_mode, float scale, int32_t dtype,
+                         int32_t kv_dtype, void* stream) {
+  Range range("gllm_paged_attention");
+  return paged_attention_impl(p, q, q_row_stride, out, out_row_stride, k_cache, v_cache, cache_slot_stride,
+                              num_blocks, block_table, block_table_stride, nullptr, 0, nullptr, 0, rope_cos,
+                              rope_sin, rope_row_stride, rope_mode, scale, dtype, kv_dtype, stream);
+}
+
+int gllm_paged_attention_write_kv(const gllm_attn_plan* p, const void* q, int64_t q_row_stride, void* out,
+                                  int64_t out_row_stride, void* k_cache, void* v_cache,
+                                  int64_t cache_slot_stride, int64_t num_blocks, const int32_t* block_table,
+                                  int64_t block_table_stride, const void* k_new, int64_t k_new_row_stride,
+                                  const void* v_new, int64_t v_new_row_stride, const void* rope_cos,
+                                  const void* rope_sin, int64_t rope_row_stride, int32_t rope_mode, float scale,
+                                  int32_t dtype, int32_t kv_dtype, void* stream) {
+  Range range("gllm_paged_attention_write_kv");
+  if (!k_new || !v_new) return fail(GLLM_ATTN_EINVAL, "null k_new / v_new");
+  return paged_attention_impl(p, q, q_row_stride, out, out_row_stride, k_cache, v_cache, cache_slot_stride,
+                              num_blocks, block_table, block_table_stride, k_new, k_new_row_stride, v_new,
+                              v_new_row_stride, rope_cos, rope_sin, rope_row_stride, rope_mode, scale, dtype,
+                              kv_dtype, stream);
 }
 
 int gllm_attention_dense(const void* q, int64_t q_row_stride, const void* k, int64_t k_batch_stride,

@@ -46,6 +46,16 @@ __device__ __forceinline__ float kvld(const KV* p) {
   else return rnd<QT>(x);
 }
 
+// A value of the model dtype stored in the cache dtype, as torch's
+// .to(kv_dtype) rounds it (to nearest even; fp8: NaN -> 0x7f|sign).
+template <typename KV> __device__ __forceinline__ KV to_kv(float x);
+template <> __device__ __forceinline__ float to_kv<float>(float x) { return x; }
+template <> __device__ __forceinline__ __bf16 to_kv<__bf16>(float x) {
+  return __builtin_bit_cast(__bf16, (uint16_t)pack_bf16x2(x, 0.f));
+}
+template <> __device__ __forceinline__ _Float16 to_kv<_Float16>(float x) { return (_Float16)x; }
+template <> __device__ __forceinline__ fp8e4m3 to_kv<fp8e4m3>(float x) { return fp8e4m3{fp8_byte(x)}; }
+
 // One 4-wave workgroup per (query head, query row, sequence).  Keys go 64 at
 // a time, chunk c to wave c % 4: lane j scores key p0 + j against q (q read
 // from LDS, so every lane has all of it), one wave max / sum per chunk
@@ -57,17 +67,27 @@ __device__ __forceinline__ float kvld(const KV* p) {
 // and V arrive in one memory round trip; NI = 4: 32 keys' V rows per batch
 // of loads, after the scores.  The four waves' (max,
 // sum, acc) merge through LDS at the end.
-template <bool DENSE, typename KV, typename QT, int NI>
+// FUSED (a.k_new != null, at most kFusedRows query rows per sequence): the
+// new tokens' K/V are written by this launch.  Every workgroup rotates and
+// casts the new keys it sees (ctx .. ctx + r) itself into LDS, the value the
+// cache round trip gives (stored in KV, read back as QT); the main loop covers
+// the cached keys [0, ctx) and wave 0 adds the new ones afterwards.  The
+// workgroup of the group's first query head and the sequence's last row
+// computes all of the sequence's new tokens and stores them at their slots
+// (block table); no workgroup of the launch reads those slots.
+constexpr int kFusedRows = 16;
+template <bool DENSE, typename KV, typename QT, int NI, bool FUSED>
 __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
   constexpr int NWV = 4;                  // waves per workgroup
   constexpr int VB = NI == 1 ? 64 : 32;   // V rows per batch of loads
   __shared__ __attribute__((aligned(16))) float qs[256];
   __shared__ float mrg[NWV][2 + 256];     // per wave: max, sum, acc[D]
+  __shared__ float nkv[2][FUSED ? kFusedRows : 1][FUSED ? 64 * NI : 1];   // new keys' K / V (FUSED)
   const int hq = blockIdx.x, r = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int D = a.head_dim;
   int ctx, qlen, L;
-  int64_t qrow;
+  int64_t qrow, row0 = 0;
   if (DENSE) {
     ctx = 0;
     qlen = a.dense_Tq;
@@ -80,6 +100,7 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
     qlen = si.q_len;
     L = ctx + qlen;
     qrow = si.q_row_start + r;
+    row0 = si.q_row_start;
   }
   if (r >= qlen) return;
   const int G = a.num_q_heads / a.num_kv_heads;
@@ -105,8 +126,50 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
     qs[d] = qv;
   }
   for (int d = D + tid; d < 64 * NI; d += 64 * NWV) qs[d] = 0.f;   // dims past D score 0
+  if constexpr (FUSED) {
+    // element pairs (token t, dims j and j + D/2); the writer takes every token
+    const bool writer = hq % G == 0 && r == qlen - 1;
+    const int nt = writer ? qlen : r + 1;
+    const int32_t* btr = a.block_table + (int64_t)b * a.block_table_stride;
+    for (int e = tid; e < nt * half; e += 64 * NWV) {
+      const int t = e / half, j = e - t * half;
+      const int64_t row = row0 + t;
+      const QT* kn = (const QT*)a.k_new + row * a.k_new_row_stride + (int64_t)kvh * D;
+      const QT* vn = (const QT*)a.v_new + row * a.v_new_row_stride + (int64_t)kvh * D;
+      float lo = (float)kn[j], hi = (float)kn[j + half];
+      if (a.rope_mode != kRopeNone) {
+        const int64_t crow = a.rope_mode == kRopeByPosition ? (int64_t)(ctx + t) : row;
+        const float c = (float)((const QT*)a.rope_cos)[crow * a.rope_row_stride + j];
+        const float sn = (float)((const QT*)a.rope_sin)[crow * a.rope_row_stride + j];
+        const float x1 = lo, x2 = hi;
+        lo = rnd<QT>(__fsub_rn(rnd<QT>(__fmul_rn(x1, c)), rnd<QT>(__fmul_rn(x2, sn))));
+        hi = rnd<QT>(__fadd_rn(rnd<QT>(__fmul_rn(x1, sn)), rnd<QT>(__fmul_rn(x2, c))));
+      }
+      const KV k1 = to_kv<KV>(lo), k2 = to_kv<KV>(hi);
+      const KV v1 = to_kv<KV>((float)vn[j]), v2 = to_kv<KV>((float)vn[j + half]);
+      if (t <= r) {
+        nkv[0][t][j] = kvld<KV, QT>(&k1);
+        nkv[0][t][j + half] = kvld<KV, QT>(&k2);
+        nkv[1][t][j] = kvld<KV, QT>(&v1);
+        nkv[1][t][j + half] = kvld<KV, QT>(&v2);
+      }
+      if (writer) {
+        const int p = ctx + t;
+        const uint32_t bi = div_bs((uint32_t)p, a.block_magic, a.block_shift);
+        const uint32_t blk = (uint32_t)btr[bi];
+        if (blk < (uint64_t)a.num_blocks) {   // never address outside the pool
+          const int64_t off = ((int64_t)blk * a.block_size + (p - (int64_t)bi * a.block_size)) * a.cache_slot_stride +
+                              (int64_t)kvh * D + j;
+          KV* kc = (KV*)a.k_cache + off;
+          KV* vc = (KV*)a.v_cache + off;
+          kc[0] = k1; kc[half] = k2;
+          vc[0] = v1; vc[half] = v2;
+        }
+      }
+    }
+  }
   __syncthreads();
-  const int nkeys = DENSE ? L : ctx + r + 1;
+  const int nkeys = DENSE ? L : (FUSED ? ctx : ctx + r + 1);
   const int32_t* bt = DENSE ? nullptr : a.block_table + (int64_t)b * a.block_table_stride;
   const KV* kbase = DENSE ? (const KV*)a.k + (int64_t)b * a.k_batch_stride + (int64_t)kvh * D
                           : (const KV*)a.k_cache + (int64_t)kvh * D;
@@ -223,6 +286,39 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
     }
     m = mn;
   }
+  if constexpr (FUSED) {
+    // the new keys ctx .. ctx + r (every one visible to row r), from LDS
+    if (wave == 0) {
+      const int nk = r + 1;
+      float s = kNegInf;
+      if (lane < nk) {
+        float dot = 0.f;
+        for (int d = 0; d < D; ++d) dot += qs[d] * nkv[0][lane][d];
+        s = dot * a.scale;
+      }
+      float cm = s;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) cm = fmaxf(cm, __shfl_xor(cm, off));
+      const float mn = fmaxf(m, cm);
+      const float alpha = expf(m - mn);
+      const float e = lane < nk ? expf(s - mn) : 0.f;
+      float es = e;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) es += __shfl_xor(es, off);
+      l = l * alpha + es;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) acc[i] *= alpha;
+      for (int u = 0; u < nk; ++u) {
+        const float pj = __shfl(e, u);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const int d = lane + 64 * i;
+          if (d < D) acc[i] += pj * nkv[1][u][d];
+        }
+      }
+      m = mn;
+    }
+  }
   // merge the waves' states (exact LSE merge; a wave without keys has
   // m = -inf and weight 0)
   if (lane == 0) {
@@ -258,22 +354,29 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnArgs a) {
   }
 }
 
+template <typename QT, int NI, bool FUSED>
+static hipError_t launch_f32_kv(const AttnArgs& a, dim3 grid, hipStream_t st) {
+  const dim3 block(256);
+  switch (a.kv_dtype) {
+    case kF32: hipLaunchKernelGGL((attn_f32_kernel<false, float, QT, NI, FUSED>), grid, block, 0, st, a); break;
+    case kBF16: hipLaunchKernelGGL((attn_f32_kernel<false, __bf16, QT, NI, FUSED>), grid, block, 0, st, a); break;
+    case kF16: hipLaunchKernelGGL((attn_f32_kernel<false, _Float16, QT, NI, FUSED>), grid, block, 0, st, a); break;
+    case kFP8: hipLaunchKernelGGL((attn_f32_kernel<false, fp8e4m3, QT, NI, FUSED>), grid, block, 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 // Cache dtype KV under model dtype QT (paged), or QT throughout (dense).
 template <typename QT, int NI>
 static hipError_t launch_f32_qt(const AttnArgs& a, bool dense, dim3 grid, hipStream_t st) {
   const dim3 block(256);
   if (dense) {
-    hipLaunchKernelGGL((attn_f32_kernel<true, QT, QT, NI>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((attn_f32_kernel<true, QT, QT, NI, false>), grid, block, 0, st, a);
     return hipGetLastError();
   }
-  switch (a.kv_dtype) {
-    case kF32: hipLaunchKernelGGL((attn_f32_kernel<false, float, QT, NI>), grid, block, 0, st, a); break;
-    case kBF16: hipLaunchKernelGGL((attn_f32_kernel<false, __bf16, QT, NI>), grid, block, 0, st, a); break;
-    case kF16: hipLaunchKernelGGL((attn_f32_kernel<false, _Float16, QT, NI>), grid, block, 0, st, a); break;
-    case kFP8: hipLaunchKernelGGL((attn_f32_kernel<false, fp8e4m3, QT, NI>), grid, block, 0, st, a); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  if (a.k_new) return launch_f32_kv<QT, NI, true>(a, grid, st);
+  return launch_f32_kv<QT, NI, false>(a, grid, st);
 }
 
 template <int NI>

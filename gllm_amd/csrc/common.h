@@ -113,6 +113,9 @@ __device__ __forceinline__ uint32_t pack_fp8x4(float a, float b, float c, float 
   return w;
 }
 
+// One value -> its fp8 byte (torch's cast, NaN -> 0x7f|sign).
+__device__ __forceinline__ uint8_t fp8_byte(float x) { return (uint8_t)(pack_fp8x4(x, 0.f, 0.f, 0.f) & 0xffu); }
+
 // 4 fp8 bytes -> 4 fp32 (exact).
 __device__ __forceinline__ void unpack_fp8x4(uint32_t w, float* v) {
   const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
@@ -218,12 +221,22 @@ __device__ __forceinline__ void round2(float& a, float& b) {
   a = E16<T>::lo(w);
   b = E16<T>::hi(w);
 }
+// Makes rounded fp16 values opaque to the optimizer, which would otherwise
+// narrow round(x1 c) - round(x2 s) to half-precision ops, which instruction
+// selection then fuses into one FMA under fp-contract=fast (a global backend
+// option, so a source pragma does not stop it), dropping the product's own
+// rounding.  No instruction is emitted.
+__device__ __forceinline__ void opaque4(float& a, float& b, float& c, float& d) {
+  asm volatile("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+}
+
 // one rotate-half pair with every op rounded to T (attention.py:105-118)
 template <typename T>
 __device__ __forceinline__ void rope_pair(float& x1, float& x2, float c, float s) {
   float a = __fmul_rn(x1, c), b = __fmul_rn(x2, s), e = __fmul_rn(x1, s), f = __fmul_rn(x2, c);
   round2<T>(a, b);
   round2<T>(e, f);
+  if constexpr (E16<T>::kF16) opaque4(a, b, e, f);   // bf16 has no half-width arithmetic to narrow to
   x1 = __fsub_rn(a, b);
   x2 = __fadd_rn(e, f);
   round2<T>(x1, x2);

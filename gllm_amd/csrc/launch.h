@@ -89,6 +89,14 @@ struct AttnArgs {
   int32_t num_q_heads, num_kv_heads, head_dim;
   float scale;
   int32_t dtype, kv_dtype;
+  // new tokens written by the attention launch itself (decode-path plans;
+  // null otherwise): row q_row_start + r of k_new / v_new (model dtype, Hkv
+  // heads at h * D) is key ctx_len + r of its sequence; k is rotated with the
+  // q rows' cos/sin rows, both are cast to the cache dtype and stored at the
+  // key's slot (block table).
+  const void* k_new;
+  const void* v_new;
+  int64_t k_new_row_stride, v_new_row_stride;
 };
 
 struct MetadataArgs {

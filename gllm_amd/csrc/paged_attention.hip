@@ -90,6 +90,57 @@ struct DecodeTask {
   int ticket;   // >= 0: counter whose last ticket merges the partials here; < 0: merge_splits does
 };
 
+// New tokens written by the attention launch (a.k_new != null): the task whose
+// key range covers key p of a new token writes that token's K (rotated like
+// apply_rope, every op rounded to T) and V, cast to the cache dtype, for its
+// HW kv heads, at the key's slot.  No other workgroup reads those bytes in
+// this launch (each key of each head belongs to one task); the workgroup
+// barrier after the prologue orders the stores before this task's own loads
+// of the key.  Element-wise stores: at most 16 tokens x HW heads x D.
+template <typename T, int D, int HW, bool KV8>
+__device__ __forceinline__ void write_new_keys(const AttnArgs& a, const DecodeTask& tk, int tid, int nthreads) {
+  const int L = tk.ctx_len + tk.q_len;
+  const int p0 = max(tk.ctx_len, tk.kbeg), p1 = min(L, tk.kend);
+  if (p0 >= p1) return;
+  constexpr int H2 = D / 2;
+  const int per_tok = HW * H2;
+  const int n = (p1 - p0) * per_tok;
+  for (int e = tid; e < n; e += nthreads) {
+    const int tok = e / per_tok, rem = e - tok * per_tok;
+    const int hh = rem / H2, j = rem - hh * H2;
+    const int kvh = tk.hg * HW + hh;
+    if (kvh >= a.num_kv_heads) continue;
+    const int p = p0 + tok;
+    const int64_t row = tk.q_row_start + (p - tk.ctx_len);
+    const T* kn = (const T*)a.k_new + row * a.k_new_row_stride + (int64_t)kvh * D;
+    const T* vn = (const T*)a.v_new + row * a.v_new_row_stride + (int64_t)kvh * D;
+    float x1 = (float)kn[j], x2 = (float)kn[j + H2];
+    if (a.rope_mode != kRopeNone) {
+      const int64_t crow = a.rope_mode == kRopeByPosition ? (int64_t)p : row;
+      const float c = (float)((const T*)a.rope_cos)[crow * a.rope_row_stride + j];
+      const float sn = (float)((const T*)a.rope_sin)[crow * a.rope_row_stride + j];
+      rope_pair<T>(x1, x2, c, sn);
+    }
+    const float v1 = (float)vn[j], v2 = (float)vn[j + H2];
+    const uint32_t bi = div_bs((uint32_t)p, a.block_magic, a.block_shift);
+    uint32_t blk = (uint32_t)a.block_table[(int64_t)tk.seq * a.block_table_stride + bi];
+    if (blk >= (uint64_t)a.num_blocks) continue;   // never address outside the pool
+    const int64_t off = ((int64_t)blk * a.block_size + (p - (int64_t)bi * a.block_size)) * a.cache_slot_stride +
+                        (int64_t)kvh * D + j;
+    if constexpr (KV8) {
+      uint8_t* kc = (uint8_t*)a.k_cache + off;
+      uint8_t* vc = (uint8_t*)a.v_cache + off;
+      kc[0] = fp8_byte(x1); kc[H2] = fp8_byte(x2);
+      vc[0] = fp8_byte(v1); vc[H2] = fp8_byte(v2);
+    } else {
+      T* kc = (T*)a.k_cache + off;
+      T* vc = (T*)a.v_cache + off;
+      kc[0] = (T)x1; kc[H2] = (T)x2;     // exact: already values of T
+      vc[0] = (T)v1; vc[H2] = (T)v2;
+    }
+  }
+}
+
 // Runs one task with every wave of the workgroup; returns with the workgroup
 // converged (no early exit), so a workgroup can run several tasks in a row.
 template <typename T, int D, int HW, int KW, bool KV8>
@@ -160,6 +211,7 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
     }
   }
   if (tid < nblk) lbid[tid] = bid < (uint64_t)a.num_blocks ? (int32_t)bid : 0;  // never address outside the pool
+  if (a.k_new) write_new_keys<T, D, HW, KV8>(a, tk, tid, 64 * NW);
 
   // Q as the B operand of S^T = K Q^T: lane holds Q[row n][chunk_dim(kk) + i].
   u32x4 qB[NK];
@@ -191,6 +243,7 @@ __device__ __forceinline__ void decode_task(const AttnArgs& a, const DecodeTask&
             float u1 = __fmul_rn(x[kk][i + 1], c[i + 1]), v1 = __fmul_rn(xp[i + 1], s[i + 1]);
             round2<T>(u0, v0);
             round2<T>(u1, v1);
+            if constexpr (E16<T>::kF16) opaque4(u0, v0, u1, v1);
             float r0 = first ? __fsub_rn(u0, v0) : __fadd_rn(u0, v0);
             float r1 = first ? __fsub_rn(u1, v1) : __fadd_rn(u1, v1);
             round2<T>(r0, r1);

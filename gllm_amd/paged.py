@@ -321,16 +321,35 @@ class AttentionPlan:
             self._h = None
 
 
+def fused_kv_write_ok(plan: AttentionPlan, kv_dtype: torch.dtype) -> bool:
+    """Whether :func:`paged_attention` can take ``kv_new`` for this plan and
+    cache dtype: every sequence on the decode path of the kernel that runs
+    (MFMA kernels: query_len x G <= 16; generic kernel: query_len <= 16)."""
+    if not plan.query_lens:
+        return False
+    mfma = (plan.dtype in (torch.bfloat16, torch.float16) and plan.head_dim in (64, 128)
+            and kv_dtype in (plan.dtype, torch.float8_e4m3fn))
+    G = plan.num_q_heads // plan.num_kv_heads
+    if mfma:
+        return max(plan.query_lens) * G <= 16
+    return max(plan.query_lens) <= 16
+
+
 def paged_attention(plan: AttentionPlan, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                     block_table: torch.Tensor, out: torch.Tensor | None = None,
-                    rope: tuple | None = None, scale: float | None = None) -> torch.Tensor:
+                    rope: tuple | None = None, scale: float | None = None,
+                    kv_new: tuple | None = None) -> torch.Tensor:
     """Attention over the paged cache for every query row in ``plan``.
 
     q ``[rows, Hq, D]`` or ``[B, T_q, Hq, D]`` (rows flattened), caches
     ``[num_slots, Hkv, D]``, block_table int32 ``[B, W]``.  ``rope`` =
     ``(cos, sin, mode)`` with mode ``"position"`` (table rows ``c_i + r``) or
     ``"row"`` (one cos/sin row per query row, the reference's gathered
-    ``cos_pos``) rotates q on load.  Returns ``out`` (same layout as q).
+    ``cos_pos``) rotates q on load.  ``kv_new`` = ``(k, v)``, one row per
+    query row in q's layout (``[..., Hkv, D]``): the new tokens' K/V, rotated
+    (k) and written into the cache at their keys' slots by the same launch
+    (``attention.py:151-161`` + this attention; the plan must pass
+    :func:`fused_kv_write_ok`).  Returns ``out`` (same layout as q).
     """
     Hq, Hkv, D = plan.num_q_heads, plan.num_kv_heads, plan.head_dim
     qs = _rows(q, Hq, D, "q")
@@ -373,6 +392,20 @@ def paged_attention(plan: AttentionPlan, q: torch.Tensor, k_cache: torch.Tensor,
     sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
     num_blocks = k_cache.shape[0] // plan.block_size
     lib = _lib.load()
+    if kv_new is not None:
+        kn, vn = kv_new
+        if kn.dtype != q.dtype or vn.dtype != q.dtype:
+            raise ValueError("k_new / v_new must be in the model dtype")
+        ks = _rows(kn, Hkv, D, "k_new")
+        vs = _rows(vn, Hkv, D, "v_new")
+        if kn.numel() // (Hkv * D) < plan.rows or vn.numel() // (Hkv * D) < plan.rows:
+            raise ValueError("k_new / v_new need one row per query row of the plan")
+        _lib.check(lib.gllm_paged_attention_write_kv(
+            plan._h, q.data_ptr(), qs, out.data_ptr(), os_, k_cache.data_ptr(), v_cache.data_ptr(),
+            k_cache.stride(0), num_blocks, block_table.data_ptr(), block_table.stride(0), kn.data_ptr(), ks,
+            vn.data_ptr(), vs, cos_p, sin_p, rs, mode, sc, _lib.dtype_code(q.dtype), _lib.dtype_code(k_cache.dtype),
+            _lib.stream_ptr(q.device)))
+        return out
     _lib.check(lib.gllm_paged_attention(
         plan._h, q.data_ptr(), qs, out.data_ptr(), os_, k_cache.data_ptr(), v_cache.data_ptr(),
         k_cache.stride(0), num_blocks, block_table.data_ptr(), block_table.stride(0), cos_p, sin_p, rs, mode,

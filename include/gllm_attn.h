@@ -252,6 +252,32 @@ int gllm_paged_attention(const gllm_attn_plan* plan, const void* q, int64_t q_ro
                          void* stream);
 
 /*
+ * gllm_rope_kv_write followed by gllm_paged_attention in one launch, for
+ * plans whose sequences are all on the decode path (query_len x G <= 16 on
+ * the MFMA kernels; query_len <= 16 on the generic kernel; other plans give
+ * GLLM_ATTN_EINVAL).  Replaces gllm/model/layers/attention.py:151-178 for a
+ * decode step (the reference's RoPE of k, its index_put_ into the cache and
+ * the attention), i.e. model.py:202-222's per-layer write + attention pair.
+ * k_new / v_new: one row per query row of q (same row layout, row strides in
+ * elements, Hkv heads at h * head_dim, model dtype).  The new key of query
+ * row r of sequence i is key c_i + r: k is rotated with the cos/sin rows
+ * rope_mode selects for q (bit-identical to apply_rope), k and v are cast to
+ * kv_dtype as .to(kv_dtype) rounds and stored at that key's slot
+ * (block_table[i][p / bs] * bs + p % bs, the reference's query_slot_mapping),
+ * and the attention reads them from there (MFMA kernels) or from the same
+ * values kept in the kernel (generic kernel).  Cache contents and outputs
+ * equal the two-call sequence's; on the MFMA kernels bit for bit.
+ */
+int gllm_paged_attention_write_kv(const gllm_attn_plan* plan, const void* q, int64_t q_row_stride,
+                                  void* out, int64_t out_row_stride, void* k_cache, void* v_cache,
+                                  int64_t cache_slot_stride, int64_t num_blocks,
+                                  const int32_t* block_table, int64_t block_table_stride,
+                                  const void* k_new, int64_t k_new_row_stride, const void* v_new,
+                                  int64_t v_new_row_stride, const void* rope_cos, const void* rope_sin,
+                                  int64_t rope_row_stride, int32_t rope_mode, float scale, int32_t dtype,
+                                  int32_t kv_dtype, void* stream);
+
+/*
  * reference_attention(q, k, v, bias): softmax(q k^T * scale + bias) v with
  * GQA.  q/out [B, T_q, Hq, D] (row stride q_row_stride, batch = T_q rows),
  * k/v [B, T, Hkv, D] with the given batch / row strides, bias [B, T_q, T]

@@ -180,3 +180,22 @@ def test_model_over_other_cache_dtype(model, cache, D):
                              b.block_table.cpu(), b.ctx_lens, b.q_lens, b.q_row_start, 16)
     if cache == F32 or (model == BF and cache == F16):
         assert (ref - raw).abs().max().item() > 1e-4
+
+
+@pytest.mark.parametrize("dtype", [BF, F16])
+@pytest.mark.parametrize("kv,D", [(None, 64), (None, 128), (F8, 64), (F8, 128)])
+def test_rope_on_load_bit_identical(dtype, kv, D):
+    """q rotated inside the attention kernels (decode and prefill items, the
+    fp8 / D = 64 decode path rotating half a pair per lane included) gives
+    the same output bits as attention over q rotated first by the RoPE
+    kernel (itself bit-exact against apply_rope)."""
+    print(f"rope on load {dtype} kv={kv} D={D}", flush=True)
+    b = _batch([10, 500, 0, 37], [1, 1, 70, 40], 32, 8, D, dtype, kv, theta=500000.0)
+    plan = paged.AttentionPlan(b.q_lens, b.seq_lens, num_q_heads=32, num_kv_heads=8, head_dim=D, block_size=16,
+                               dtype=dtype, device=DEV)
+    pos = torch.cat([torch.arange(c, c + q) for c, q in zip(b.ctx_lens, b.q_lens)]).to(DEV)
+    out1 = paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table, rope=(b.cos, b.sin, "position"))
+    qr = paged.rope_rotate(b.q, b.cos, b.sin, rope_rows=pos)
+    out2 = paged.paged_attention(plan, qr, b.k_cache, b.v_cache, b.block_table)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(out1), _bits(out2))
