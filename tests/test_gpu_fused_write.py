@@ -118,3 +118,81 @@ def test_fused_write_rejects_prefill_plans():
     with pytest.raises(ValueError, match="decode-path"):
         paged.paged_attention(plan, b.q, b.k_cache, b.v_cache, b.block_table, rope=(cs, sn, "row"),
                               kv_new=(b.k_new, b.v_new))
+
+
+@pytest.mark.parametrize("bs", [1, 7, 64])
+@pytest.mark.parametrize("dtype,kv,D", [(torch.bfloat16, None, 128), (torch.bfloat16, torch.float8_e4m3fn, 64),
+                                        (torch.float32, None, 64)])
+def test_fused_write_block_sizes(bs, dtype, kv, D):
+    """Block sizes other than 16 (the slot comes from the block table at key
+    position c_i + r through the plan's block-size division): output and
+    cache against the two calls, on the MFMA and the generic kernel."""
+    print(f"fused write bs={bs} {dtype} kv={kv} D={D}", flush=True)
+    b, plan, cs, sn, rr = _case([40, 700, 0, 130, 15], [1, 1, 1, 2, 1], 32, 8, D, dtype, kv, bs=bs)
+    o1, o2, c1, c2 = _run_both(b, plan, cs, sn, rr, "row")
+    assert torch.equal(_bits(c1[0]), _bits(c2[0])) and torch.equal(_bits(c1[1]), _bits(c2[1]))
+    if dtype == torch.float32:
+        assert (o1 - o2).abs().max().item() < 2e-6
+    else:
+        assert torch.equal(_bits(o1), _bits(o2))
+
+
+def test_fused_write_in_attention_forward_graph():
+    """gllm_amd.Attention on a decode step takes the fused path; the step
+    captured in a HIP graph and replayed matches eager bit for bit (outputs
+    and the written cache)."""
+    import gllm_amd
+    print("fused write attention graph", flush=True)
+    L, Hq, Hkv, D, bs, B = 2, 32, 8, 64, 16, 4
+    ctx = [30, 200, 5, 77]
+    seq = [c + 1 for c in ctx]
+    cache = gllm_amd.PagedKVCache(L, Hkv, D, bs, B, 256, torch.bfloat16, DEV)
+    cache.physical_kv_cache.normal_()
+    bt = workloads.block_tables(seq, bs, cache.num_blocks).to(DEV)
+    pos = torch.tensor(ctx)
+    qsm = (bt.cpu()[torch.arange(B), pos // bs].to(torch.int64) * bs + pos % bs).view(B, 1).to(DEV)
+    meta = gllm_amd.AttentionMetadata(query_lens=torch.ones(B, dtype=torch.int32, device=DEV),
+                                      seq_lens=torch.tensor(seq, dtype=torch.int32, device=DEV), max_seq_len=max(seq),
+                                      block_table=bt, slot_mapping=None, query_slot_mapping=qsm, bias=None,
+                                      block_size=bs)
+    ang = pos.unsqueeze(1) * 500000.0 ** (-2 * torch.arange(D // 2) / D)
+    cos = torch.cos(ang).to(torch.bfloat16).view(B, 1, -1).to(DEV)
+    sin = torch.sin(ang).to(torch.bfloat16).view(B, 1, -1).to(DEV)
+
+    class Cfg:
+        num_attn_heads, num_kv_heads, head_dim, hidden_size, dtype = Hq, Hkv, D, Hq * D, torch.bfloat16
+
+    atts = [gllm_amd.Attention(li, Cfg, {f"model.layers.{li}.self_attn.{n}_proj.weight": torch.zeros(1)
+                                         for n in "qkvo"}) for li in range(L)]
+    g = torch.Generator(device=DEV).manual_seed(5)
+    qs = [torch.randn(B, 1, Hq, D, device=DEV, generator=g).to(torch.bfloat16) for _ in range(L)]
+    ks = [torch.randn(B, 1, Hkv, D, device=DEV, generator=g).to(torch.bfloat16) for _ in range(L)]
+    vs = [torch.randn(B, 1, Hkv, D, device=DEV, generator=g).to(torch.bfloat16) for _ in range(L)]
+    pristine = cache.physical_kv_cache.clone()
+
+    def step():
+        return [atts[li].attention(qs[li], ks[li], vs[li], cos, sin, cache.get_layer_kv_cache(li), meta)
+                for li in range(L)]
+
+    eager = [o.clone() for o in step()]
+    torch.cuda.synchronize()
+    assert paged.fused_kv_write_ok(meta._gllm_plan, torch.bfloat16)
+    eager_cache = cache.physical_kv_cache.clone()
+    cache.physical_kv_cache.copy_(pristine)
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()                                    # warm up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        outs = step()
+    for _ in range(3):
+        cache.physical_kv_cache.copy_(pristine)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(_bits(o), _bits(e))
+        assert torch.equal(_bits(cache.physical_kv_cache), _bits(eager_cache))
