@@ -147,10 +147,44 @@ def test_qkv_rejects_bad_arguments():
     sl = torch.arange(4, dtype=torch.int64, device=DEV)
     with pytest.raises(NotImplementedError):
         paged.qkv_rope_kv_write(x, None, w, w, cs, cs, kc, kc.clone(), sl)
+    # the fused kernel projects in bf16 MFMA: its C entry point refuses other
+    # model dtypes (the Python entry routes them to F.linear + the RoPE/KV
+    # write kernel, test_qkv_other_model_dtypes_unfused_route)
+    from gllm_amd import _lib
+    lib = _lib.load()
     x32 = torch.zeros(4, 128, dtype=torch.float32, device=DEV)
     w32 = torch.zeros(128, 128, dtype=torch.float32, device=DEV)
-    with pytest.raises(NotImplementedError):
-        paged.qkv_rope_kv_write(x32, None, w32, w32, cs.float(), cs.float(), kc.float(), kc.float().clone(), sl)
+    kc32, cs32 = kc.float(), cs.float()
+    rc = lib.gllm_qkv_rope_kv_write(
+        x32.data_ptr(), 128, 4, 128, None, 0, w32.data_ptr(), 128, w32.data_ptr(), 128, None, 0, 0,
+        kc32.data_ptr(), kc32.clone().data_ptr(), 128, 16, sl.data_ptr(), None, 1, cs32.data_ptr(), cs32.data_ptr(),
+        None, 64, 1, 1, 128, _lib.dtype_code(torch.float32), _lib.dtype_code(torch.float32), None, 0,
+        _lib.stream_ptr(x32.device))
+    assert rc == 2, rc                                   # GLLM_ATTN_EUNSUPPORTED
+
+
+@pytest.mark.parametrize("dtype,kvd", [(torch.float32, torch.float32), (torch.float16, torch.float16),
+                                       (torch.float32, torch.bfloat16)])
+def test_qkv_other_model_dtypes_unfused_route(dtype, kvd):
+    """fp32 and fp16 models (the reference takes any model dtype,
+    model.py:64): the projections run as F.linear in the model dtype and
+    the RoPE/KV write kernel rotates and stores.  Small integer data keep
+    every product and sum exact, so q and the caches match the oracle bit
+    for bit."""
+    print(f"qkv unfused {dtype} kv={kvd}", flush=True)
+    n, hidden, Hq, Hkv, D = 24, 512, 8, 2, 64
+    x, w, cos_t, sin_t, pos, slots, num_slots = _inputs(n, hidden, Hq, Hkv, D, True, 77)
+    x, w = x.to(dtype), [t.to(dtype) for t in w]
+    cos_t, sin_t = orope.rope_cache(4096, D, 500000.0, dtype)
+    kc_ref = torch.zeros(num_slots, Hkv, D, dtype=kvd)
+    vc_ref = torch.zeros_like(kc_ref)
+    qr = op.qkv_rope_kv_write(x, w[0], w[1], w[2], cos_t[pos], sin_t[pos], kc_ref, vc_ref, slots, Hkv, D)
+    kc, vc = torch.zeros_like(kc_ref, device=DEV), torch.zeros_like(vc_ref, device=DEV)
+    q = paged.qkv_rope_kv_write(x.to(DEV), w[0].to(DEV), w[1].to(DEV), w[2].to(DEV), cos_t.to(DEV), sin_t.to(DEV),
+                                kc, vc, slots.to(DEV), rope_rows=pos.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(q.cpu(), qr)
+    assert torch.equal(kc.cpu(), kc_ref) and torch.equal(vc.cpu(), vc_ref)
 
 
 # hidden 544 (not a multiple of 64): the partial kernel's 32-wide K steps
